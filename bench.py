@@ -1,0 +1,172 @@
+#!/usr/bin/env python3
+"""INT8 InferenceSession throughput on one MI355X.
+
+Default workload: the 4096^2 Linear stack (4 x Linear 4096->4096 + GELU,
+input f32 [8192, 4096], seeded xavier weights), on which the metric's
+"% of i8 MFMA peak" is quoted.  A step is one InferenceSession run over the
+whole batch with the input already resident in HBM: per layer the absmax /
+quantize kernels, the i8 MFMA GEMM with its fused dequant+bias+GELU
+epilogue, all on the session's HIP stream.  The timed region is K runs back
+to back bracketed by HIP events (rgnpu_program_benchmark); every run also
+records per-op events, so the dominant kernel's mean duration comes from the
+same region.
+
+Prints one JSON line (driver contract): value = samples/s of the whole job,
+roofline = the dominant kernel against the MI355X peak, cpu_baseline = the
+C restatement of the reference's rayon CPU path timed on a bounded sample on
+this host.  --workload gemv selects the batch-1 GEMV decode shape (HBM
+roofline) for measurement runs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "INT8 InferenceSession samples/s; achieved TOPS as % of i8 MFMA peak"
+PEAK_I8_TOPS = 5000.0     # MI355X dense i8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+
+
+def build_workload(name: str, batch: int):
+    from rustgears_amd import configs
+    if name == "linear_stack":
+        model, x = configs.linear_stack()
+        return model.export(), x, {"workload": "linear_stack_4x4096_gelu", "rows": 8192, "width": 4096,
+                                   "depth": 4, "activation": "GELU", "global_batch": 8192}
+    if name == "gemv":
+        layers, x = configs.gemv(batch=batch)
+        return layers, x, {"workload": f"gemv_8192x28672_silu_b{batch}", "batch": batch, "d": 8192, "h": 28672,
+                           "global_batch": batch}
+    if name == "deep_mlp":
+        model, x = configs.deep_mlp()
+        return model.export(), x, {"workload": "deep_mlp_784_1024_1024_10", "rows": 4096, "global_batch": 4096}
+    if name == "cnn":
+        model, x = configs.cnn()
+        return model.export(), x, {"workload": "cnn_3x32x32", "images": 256, "global_batch": 256}
+    if name == "quickstart":
+        model, x = configs.quickstart()
+        return model.export(), x, {"workload": "quickstart_mlp", "rows": 64, "global_batch": 64}
+    raise SystemExit(f"unknown workload {name}")
+
+
+def dominant_roofline(name, records, layers, x, steps_records):
+    """Roofline of the dominant kernel (largest total kernel time per step)."""
+    best = max(range(len(records)), key=lambda i: records[i].kernel_ns)
+    r = records[best]
+    if r.kernel_ns <= 0:
+        return None, best
+    secs = r.kernel_ns / 1e9
+    if name == "gemv":
+        # algorithmic bytes of one GEMV launch: i8 weights N*K + f32 bias N +
+        # i8 activations B*K + f32 output B*N (the weight stream dominates)
+        lin = [l for l in layers if type(l).__name__ == "Linear"]
+        idx = [i for i, rr in enumerate(records) if "Gemm" in rr.op][: len(lin)]
+        li = lin[idx.index(best)] if best in idx else lin[0]
+        b = x.shape[0]
+        byts = li.in_features * li.out_features + 4 * li.out_features + b * li.in_features + 4 * b * li.out_features
+        ach = byts / secs / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": r.op,
+                "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
+    ops = 2 * r.macs
+    ach = ops / secs / 1e12
+    return {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
+            "frac": round(ach / PEAK_I8_TOPS, 4), "traffic": None, "kernel": r.op,
+            "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
+
+
+def cpu_baseline(name, layers, x, target_s: float):
+    """The oracle (C restatement of the reference's rayon INT8 path) on a
+    bounded row sample of the same workload, all host threads."""
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    prog = oracle.RefProgram(layers)
+    n = x.shape[0]
+    rows = max(1, min(n, 8 if name != "gemv" else n))
+    t0 = time.perf_counter()
+    prog.run(x[:rows], parallel=True)
+    dt = time.perf_counter() - t0
+    if name != "gemv" and dt < target_s / 4 and rows < n:
+        rows = int(min(n, max(rows, rows * target_s / max(dt, 1e-6) * 0.8)))
+        t0 = time.perf_counter()
+        prog.run(x[:rows], parallel=True)
+        dt = time.perf_counter() - t0
+    eff = min(rows, threads)
+    return {"value": round(rows / dt, 3), "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {n} samples of the same workload, one pass ({dt:.1f} s); "
+                      f"row-parallel like rayon, effective parallelism min(rows, threads) = {eff}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="linear_stack",
+                    choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart"])
+    ap.add_argument("--batch", type=int, default=1, help="gemv batch (1 or 8)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (sharding is described in "
+                                   "DESIGN.md, not run)"}))
+        sys.exit(2)
+
+    import rustgears_amd as rg
+
+    t_setup = time.perf_counter()
+    layers, x, config = build_workload(args.workload, args.batch)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    out_shape = sess.output_shape(x.shape)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(int(np.prod(out_shape)) * 4)
+    print(f"# setup {time.perf_counter() - t_setup:.1f}s; {sess.compilation_report().splitlines()[1].strip()}",
+          file=sys.stderr, flush=True)
+
+    if args.warmup > 0:
+        sess.benchmark(dx, x.shape, dy, args.warmup, per_kernel_events=False)
+    rg.lib().rgnpu_device_synchronize()
+    w0 = time.perf_counter()
+    dev_ms, recs = sess.benchmark(dx, x.shape, dy, args.steps, per_kernel_events=True)
+    rg.lib().rgnpu_device_synchronize()
+    wall = time.perf_counter() - w0
+    ms_per_step = dev_ms / args.steps
+    # same region without per-op events, to show their cost
+    dev_ms_noev, _ = sess.benchmark(dx, x.shape, dy, args.steps, per_kernel_events=False)
+
+    batch = x.shape[0]
+    value = batch / (ms_per_step / 1e3)
+    total_macs = sum(r.macs for r in recs)
+    tops = 2 * total_macs / (ms_per_step / 1e3) / 1e12
+    roof, dom = dominant_roofline(args.workload, recs, layers, x, recs)
+    for r in recs:
+        print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
+              file=sys.stderr)
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8",
+        "data": "synthetic: RustGears SplitMix64 seeded weights and inputs (rustgears_amd/configs.py)",
+        "config": config,
+        "tops": round(tops, 2), "tops_frac_of_i8_peak": round(tops / PEAK_I8_TOPS, 4),
+        "ms_per_step_without_op_events": round(dev_ms_noev / args.steps, 4),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": roof,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

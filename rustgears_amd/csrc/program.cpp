@@ -1,0 +1,1078 @@
+// program.cpp — host runtime of the MI355X INT8 execution provider.
+//
+// compile  (npu::compile, src/inference/npu.rs:188-276): fold_batch_norm
+//          (src/inference/mod.rs:225-257), Linear/Conv2d + Activation fusion,
+//          per-tensor i8 weight quantization (quantize.rs:18-24), weight
+//          upload in the padded [Npad, Kpad] device layout.
+// run      (NpuProgram::execute, npu.rs:296-421): a per-input-shape plan fixes
+//          buffers, absmax slots and kernel choices; every op is enqueued on
+//          the program's single HIP stream.
+// The host arithmetic here (BN folding, weight quantization) is written as
+// separate f32 operations and compiled with -ffp-contract=off so it rounds
+// exactly like the reference.
+#include <hip/hip_runtime_api.h>
+
+#include <charconv>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/rgnpu.h"
+#include "devmath.h"
+#include "rgnpu_internal.h"
+
+namespace rgnpu {
+
+thread_local std::string g_last_error;
+
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define RG_HIP(expr)                                                                       \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      throw Error(RGNPU_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));   \
+  } while (0)
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+  void ensure(size_t n) {
+    if (n <= bytes && p) return;
+    release();
+    size_t b = n ? n : 16;
+    RG_HIP(hipMalloc(&p, b));
+    bytes = b;
+  }
+  template <class T>
+  T* as() const { return static_cast<T*>(p); }
+};
+
+// ---- label formatting (Display impls, mod.rs:56-67, npu.rs:83-104) ---------
+static std::string rust_f32(float v) {
+  if (v != v) return "NaN";
+  if (std::isinf(v)) return v < 0 ? "-inf" : "inf";
+  char buf[128];
+  auto res = std::to_chars(buf, buf + sizeof buf, v, std::chars_format::fixed);
+  return std::string(buf, res.ptr);
+}
+
+static std::string act_display(int act, float p) {
+  switch (act) {
+    case rgmath::ACT_NONE: return "none";
+    case rgmath::ACT_RELU: return "ReLU";
+    case rgmath::ACT_SIGMOID: return "Sigmoid";
+    case rgmath::ACT_TANH: return "Tanh";
+    case rgmath::ACT_GELU: return "GELU";
+    case rgmath::ACT_LEAKY_RELU: return "LeakyReLU(" + rust_f32(p) + ")";
+    case rgmath::ACT_SILU: return "SiLU";
+  }
+  return "?";
+}
+
+enum OpKind { OP_LINEAR = 1, OP_CONV = 2, OP_POOL = 4, OP_FLATTEN = 5, OP_ACT = 6, OP_SOFTMAX = 7 };
+
+struct Op {
+  int kind = 0;
+  int64_t in_f = 0, out_f = 0;  // Linear features / Conv2d channels
+  int64_t k = 0, s = 0, p = 0;  // Conv2d kernel/stride/pad, MaxPool2d kernel/stride
+  int act = 0;
+  float act_param = 0.0f;
+  std::vector<int8_t> wq;  // [out, K] as the reference holds it
+  float w_scale = 1.0f;
+  std::vector<float> bias;
+  int64_t K = 0, Kpad = 0, Npad = 0;
+  DevBuf d_w, d_bias;
+  std::string label;
+};
+
+enum { BUF_INPUT = -1, BUF_OUTPUT = -2 };
+
+struct OpPlan {
+  std::vector<int64_t> in_shape, out_shape;
+  int64_t in_len = 0, out_len = 0;
+  int in_buf = BUF_INPUT, out_buf = BUF_OUTPUT;
+  uint64_t macs = 0;
+  int64_t rows = 0, Mpad = 0;
+  bool gemv = false;
+  ConvShape cs{};
+  bool full_cov = true;
+  int64_t mask_off = 0;       // offset of row/col coverage masks in Plan::masks
+  int64_t slot_base = -1, slot_count = 0;
+  bool explicit_absmax = true;
+  int64_t emit_slot = -1;     // this op's kernel writes absmax into slots[emit_slot..]
+  int emit_per_image = 0;
+};
+
+struct Plan {
+  std::vector<int64_t> in_shape, out_shape;
+  int64_t in_len = 0, out_len = 0;
+  std::vector<OpPlan> ops;
+  size_t f32_elems = 0, q_bytes = 0;
+  int64_t n_slots = 0;
+  DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
+  std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
+  bool capture_ready = false;
+};
+
+}  // namespace rgnpu
+
+using namespace rgnpu;
+
+struct rgnpu_program {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int64_t original_layers = 0;
+  int64_t fp32_bytes = 0, npu_bytes = 0;
+  std::vector<std::unique_ptr<Op>> ops;
+  std::unique_ptr<Plan> plan;
+  int profiling = 1;
+  bool capture = false;
+  bool capture_valid = false;
+  std::vector<hipEvent_t> ev;  // run start/end + 4 per op
+  bool profile_pending = false;
+  bool have_profile = false;
+  rgnpu_profile prof{};
+  std::vector<rgnpu_op_record> records;
+  std::mutex mu;
+};
+
+namespace rgnpu {
+
+static void check_layer(const rgnpu_layer& l, int64_t idx) {
+  auto bad = [&](const std::string& m) { throw Error(RGNPU_ERR_INVALID, "layer " + std::to_string(idx) + ": " + m); };
+  switch (l.kind) {
+    case RGNPU_LAYER_LINEAR:
+      if (l.in_features <= 0 || l.out_features <= 0) bad("Linear needs positive in/out features");
+      if (l.weight_len != (int64_t)l.in_features * l.out_features || !l.weight) bad("Linear weight must be [in, out]");
+      if (l.bias_len != l.out_features || !l.bias) bad("Linear bias must have out_features elements");
+      break;
+    case RGNPU_LAYER_CONV2D:
+      if (l.in_channels <= 0 || l.out_channels <= 0 || l.kernel <= 0 || l.stride <= 0 || l.padding < 0)
+        bad("Conv2d needs positive channels/kernel/stride and padding >= 0");
+      if (l.weight_len != (int64_t)l.out_channels * l.in_channels * l.kernel * l.kernel || !l.weight)
+        bad("Conv2d weight must be [out, in, k, k]");
+      if (l.bias_len != l.out_channels || !l.bias) bad("Conv2d bias must have out_channels elements");
+      break;
+    case RGNPU_LAYER_CHANNEL_AFFINE:
+      if (l.affine_len <= 0 || !l.scale || !l.shift) bad("ChannelAffine needs scale and shift");
+      break;
+    case RGNPU_LAYER_MAXPOOL2D:
+      if (l.pool_kernel <= 0 || l.pool_stride <= 0) bad("MaxPool2d needs positive kernel and stride");
+      break;
+    case RGNPU_LAYER_FLATTEN:
+    case RGNPU_LAYER_SOFTMAX:
+      break;
+    case RGNPU_LAYER_ACTIVATION:
+      if (l.act < RGNPU_ACT_NONE || l.act > RGNPU_ACT_SILU) bad("unknown activation code");
+      break;
+    default:
+      bad("unknown layer kind");
+  }
+}
+
+// Folded layer (owning copies), fold_batch_norm (inference/mod.rs:225-257).
+struct FLayer {
+  rgnpu_layer spec{};
+  std::vector<float> w, b, scale, shift;
+};
+
+static std::vector<FLayer> fold_batch_norm(const rgnpu_layer* L, int64_t n) {
+  std::vector<FLayer> out;
+  out.reserve((size_t)n);
+  for (int64_t i = 0; i < n; i++) {
+    const rgnpu_layer& l = L[i];
+    if (l.kind == RGNPU_LAYER_CHANNEL_AFFINE && !out.empty()) {
+      FLayer& last = out.back();
+      if (last.spec.kind == RGNPU_LAYER_LINEAR && last.spec.out_features == l.affine_len) {
+        const int64_t in = last.spec.in_features, of = last.spec.out_features;
+        for (int64_t r = 0; r < in; r++)
+          for (int64_t c = 0; c < of; c++) last.w[r * of + c] = last.w[r * of + c] * l.scale[c];
+        for (int64_t c = 0; c < of; c++) {
+          const float t = last.b[c] * l.scale[c];
+          last.b[c] = t + l.shift[c];
+        }
+        continue;
+      }
+      if (last.spec.kind == RGNPU_LAYER_CONV2D && last.spec.out_channels == l.affine_len) {
+        const int64_t plane = (int64_t)last.spec.in_channels * last.spec.kernel * last.spec.kernel;
+        for (int64_t o = 0; o < last.spec.out_channels; o++) {
+          for (int64_t j = 0; j < plane; j++) last.w[o * plane + j] = last.w[o * plane + j] * l.scale[o];
+          const float t = last.b[o] * l.scale[o];
+          last.b[o] = t + l.shift[o];
+        }
+        continue;
+      }
+    }
+    FLayer f;
+    f.spec = l;
+    if (l.kind == RGNPU_LAYER_LINEAR || l.kind == RGNPU_LAYER_CONV2D) {
+      f.w.assign(l.weight, l.weight + l.weight_len);
+      f.b.assign(l.bias, l.bias + l.bias_len);
+    } else if (l.kind == RGNPU_LAYER_CHANNEL_AFFINE) {
+      f.scale.assign(l.scale, l.scale + l.affine_len);
+      f.shift.assign(l.shift, l.shift + l.affine_len);
+    }
+    out.push_back(std::move(f));
+  }
+  return out;
+}
+
+// QuantTensor::from_f32 (quantize.rs:18-24) on the host.
+static float quantize_host(const float* v, int64_t n, int8_t* out) {
+  float max_abs = 0.0f;
+  for (int64_t i = 0; i < n; i++) max_abs = std::fmax(max_abs, std::fabs(v[i]));
+  const float scale = rgmath::scale_from_absmax(max_abs);
+  const float inv = 1.0f / scale;
+  for (int64_t i = 0; i < n; i++) out[i] = rgmath::quantize_one(v[i], inv);
+  return scale;
+}
+
+static void upload_weights(Op& op, hipStream_t s) {
+  // [N, K] host -> [Npad, Kpad] device, zero padded.
+  std::vector<int8_t> pad((size_t)(op.Npad * op.Kpad), 0);
+  for (int64_t r = 0; r < op.out_f; r++) std::memcpy(&pad[(size_t)(r * op.Kpad)], &op.wq[(size_t)(r * op.K)], (size_t)op.K);
+  std::vector<float> bpad((size_t)op.Npad, 0.0f);
+  std::memcpy(bpad.data(), op.bias.data(), sizeof(float) * op.bias.size());
+  op.d_w.ensure(pad.size());
+  op.d_bias.ensure(bpad.size() * sizeof(float));
+  RG_HIP(hipMemcpyAsync(op.d_w.p, pad.data(), pad.size(), hipMemcpyHostToDevice, s));
+  RG_HIP(hipMemcpyAsync(op.d_bias.p, bpad.data(), bpad.size() * sizeof(float), hipMemcpyHostToDevice, s));
+  RG_HIP(hipStreamSynchronize(s));
+}
+
+static std::string op_label(const Op& op) {
+  const std::string a = act_display(op.act, op.act_param);
+  char buf[256];
+  switch (op.kind) {
+    case OP_LINEAR:
+      if (op.act == rgmath::ACT_NONE)
+        snprintf(buf, sizeof buf, "NPU::Gemm(%lld->%lld)", (long long)op.in_f, (long long)op.out_f);
+      else
+        snprintf(buf, sizeof buf, "NPU::FusedGemmAct(%lld->%lld, %s)", (long long)op.in_f, (long long)op.out_f, a.c_str());
+      break;
+    case OP_CONV:
+      if (op.act == rgmath::ACT_NONE)
+        snprintf(buf, sizeof buf, "NPU::Conv2d(%lld->%lld, k=%lld)", (long long)op.in_f, (long long)op.out_f, (long long)op.k);
+      else
+        snprintf(buf, sizeof buf, "NPU::FusedConv2dAct(%lld->%lld, k=%lld, %s)", (long long)op.in_f, (long long)op.out_f,
+                 (long long)op.k, a.c_str());
+      break;
+    case OP_POOL: snprintf(buf, sizeof buf, "NPU::MaxPool2d(k=%lld)", (long long)op.k); break;
+    case OP_FLATTEN: snprintf(buf, sizeof buf, "NPU::Flatten"); break;
+    case OP_ACT: snprintf(buf, sizeof buf, "NPU::Act(%s)", a.c_str()); break;
+    case OP_SOFTMAX: snprintf(buf, sizeof buf, "NPU::Softmax"); break;
+    default: snprintf(buf, sizeof buf, "?");
+  }
+  return buf;
+}
+
+// npu::compile (npu.rs:188-276).
+static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
+  for (int64_t i = 0; i < n; i++) check_layer(layers[i], i);
+  P->original_layers = n;
+  std::vector<FLayer> F = fold_batch_norm(layers, n);
+  size_t i = 0;
+  while (i < F.size()) {
+    const bool has_act = i + 1 < F.size() && F[i + 1].spec.kind == RGNPU_LAYER_ACTIVATION;
+    auto op = std::make_unique<Op>();
+    const FLayer& f = F[i];
+    if (f.spec.kind == RGNPU_LAYER_LINEAR || f.spec.kind == RGNPU_LAYER_CONV2D) {
+      op->act = has_act ? F[i + 1].spec.act : rgmath::ACT_NONE;
+      op->act_param = has_act ? F[i + 1].spec.act_param : 0.0f;
+      if (has_act) i++;
+    }
+    if (f.spec.kind == RGNPU_LAYER_LINEAR) {
+      op->kind = OP_LINEAR;
+      op->in_f = f.spec.in_features;
+      op->out_f = f.spec.out_features;
+      op->K = op->in_f;
+      // transpose2d [in,out] -> [out,in] (npu.rs:208), then per-tensor quantize.
+      std::vector<float> wt((size_t)(op->in_f * op->out_f));
+      for (int64_t r = 0; r < op->in_f; r++)
+        for (int64_t c = 0; c < op->out_f; c++) wt[(size_t)(c * op->in_f + r)] = f.w[(size_t)(r * op->out_f + c)];
+      op->wq.resize(wt.size());
+      op->w_scale = quantize_host(wt.data(), (int64_t)wt.size(), op->wq.data());
+      op->bias = f.b;
+      P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
+      P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
+      op->Npad = round_up(op->out_f, kRowPad);
+      op->Kpad = round_up(op->K, kKPad);
+    } else if (f.spec.kind == RGNPU_LAYER_CONV2D) {
+      op->kind = OP_CONV;
+      op->in_f = f.spec.in_channels;
+      op->out_f = f.spec.out_channels;
+      op->k = f.spec.kernel;
+      op->s = f.spec.stride;
+      op->p = f.spec.padding;
+      op->K = op->in_f * op->k * op->k;
+      op->wq.resize(f.w.size());
+      op->w_scale = quantize_host(f.w.data(), (int64_t)f.w.size(), op->wq.data());  // [out, c*k*k] (npu.rs:231)
+      op->bias = f.b;
+      P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
+      P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
+      op->Npad = round_up(op->out_f, kConvOPad);
+      op->Kpad = round_up(op->K, kKPad);
+    } else if (f.spec.kind == RGNPU_LAYER_CHANNEL_AFFINE) {
+      // Lone ChannelAffine -> diagonal Linear, no byte accounting (npu.rs:254-270).
+      const int64_t c = (int64_t)f.scale.size();
+      std::vector<float> w((size_t)(c * c), 0.0f);
+      for (int64_t j = 0; j < c; j++) w[(size_t)(j * c + j)] = f.scale[(size_t)j];
+      op->kind = OP_LINEAR;
+      op->in_f = op->out_f = op->K = c;
+      op->act = rgmath::ACT_NONE;
+      op->wq.resize(w.size());
+      op->w_scale = quantize_host(w.data(), (int64_t)w.size(), op->wq.data());
+      op->bias = f.shift;
+      op->Npad = round_up(c, kRowPad);
+      op->Kpad = round_up(c, kKPad);
+    } else if (f.spec.kind == RGNPU_LAYER_MAXPOOL2D) {
+      op->kind = OP_POOL;
+      op->k = f.spec.pool_kernel;
+      op->s = f.spec.pool_stride;
+    } else if (f.spec.kind == RGNPU_LAYER_FLATTEN) {
+      op->kind = OP_FLATTEN;
+    } else if (f.spec.kind == RGNPU_LAYER_ACTIVATION) {
+      op->kind = OP_ACT;
+      op->act = f.spec.act;
+      op->act_param = f.spec.act_param;
+    } else if (f.spec.kind == RGNPU_LAYER_SOFTMAX) {
+      op->kind = OP_SOFTMAX;
+    }
+    if (op->kind == OP_LINEAR || op->kind == OP_CONV) upload_weights(*op, P->stream);
+    op->label = op_label(*op);
+    P->ops.push_back(std::move(op));
+    i++;
+  }
+}
+
+static int64_t out_size(int64_t input, int64_t k, int64_t s, int64_t pad) {  // kernels.rs:10-15
+  const int64_t padded = input + 2 * pad;
+  if (padded < k) throw Error(RGNPU_ERR_SHAPE, "kernel " + std::to_string(k) + " larger than padded input " + std::to_string(padded));
+  return (padded - k) / s + 1;
+}
+
+// Coverage of one spatial axis by the conv windows: position i is read by
+// some window iff i = o*s + t - pad for o < out, t < k.
+static std::vector<uint8_t> coverage(int64_t size, int64_t k, int64_t s, int64_t pad, int64_t out) {
+  std::vector<uint8_t> m((size_t)size, 0);
+  for (int64_t o = 0; o < out; o++)
+    for (int64_t t = 0; t < k; t++) {
+      const int64_t i = o * s + t - pad;
+      if (i >= 0 && i < size) m[(size_t)i] = 1;
+    }
+  return m;
+}
+
+static int64_t numel(const std::vector<int64_t>& s) {
+  int64_t n = 1;
+  for (int64_t v : s) n *= v;
+  return n;
+}
+
+static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
+  if (ndim < 1 || ndim > 8) throw Error(RGNPU_ERR_SHAPE, "input rank must be 1..8");
+  auto plan = std::make_unique<Plan>();
+  plan->in_shape.assign(shape, shape + ndim);
+  for (int64_t v : plan->in_shape)
+    if (v < 0) throw Error(RGNPU_ERR_SHAPE, "negative dimension");
+  plan->in_len = numel(plan->in_shape);
+  std::vector<int64_t> cur = plan->in_shape;
+  std::vector<uint8_t> mask_host;
+  const size_t nops = P->ops.size();
+  plan->ops.resize(nops);
+  for (size_t i = 0; i < nops; i++) {
+    const Op& op = *P->ops[i];
+    OpPlan& pl = plan->ops[i];
+    pl.in_shape = cur;
+    pl.in_len = numel(cur);
+    switch (op.kind) {
+      case OP_LINEAR: {  // npu.rs:307-318
+        if (pl.in_len % op.in_f != 0)
+          throw Error(RGNPU_ERR_SHAPE, "Linear(" + std::to_string(op.in_f) + "): input length " + std::to_string(pl.in_len) +
+                                           " is not a multiple of in_features");
+        pl.rows = pl.in_len / op.in_f;
+        pl.macs = (uint64_t)(pl.rows * op.in_f * op.out_f);
+        pl.Mpad = round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
+        pl.gemv = pl.rows <= 8;
+        cur.back() = op.out_f;
+        break;
+      }
+      case OP_CONV: {  // npu.rs:319-383
+        if (cur.size() < 4) throw Error(RGNPU_ERR_SHAPE, "Conv2d expects NCHW input");
+        const int64_t n = cur[0], c = cur[1], h = cur[2], w = cur[3];
+        if (c != op.in_f)
+          throw Error(RGNPU_ERR_SHAPE, "Conv2d: input has " + std::to_string(c) + " channels, expected " + std::to_string(op.in_f));
+        const int64_t oh = out_size(h, op.k, op.s, op.p), ow = out_size(w, op.k, op.s, op.p);
+        pl.cs = ConvShape{n, c, h, w, op.out_f, op.Npad, op.k, op.s, op.p, oh, ow, op.Kpad};
+        pl.macs = (uint64_t)(n * op.out_f * op.K * oh * ow);
+        auto rm = coverage(h, op.k, op.s, op.p, oh), cm = coverage(w, op.k, op.s, op.p, ow);
+        pl.full_cov = true;
+        for (auto v : rm) pl.full_cov &= v != 0;
+        for (auto v : cm) pl.full_cov &= v != 0;
+        pl.mask_off = (int64_t)mask_host.size();
+        mask_host.insert(mask_host.end(), rm.begin(), rm.end());
+        mask_host.insert(mask_host.end(), cm.begin(), cm.end());
+        cur = {n, op.out_f, oh, ow};
+        break;
+      }
+      case OP_POOL: {  // npu.rs:384-390
+        if (cur.size() < 4) throw Error(RGNPU_ERR_SHAPE, "MaxPool2d expects NCHW input");
+        const int64_t oh = out_size(cur[2], op.k, op.s, 0), ow = out_size(cur[3], op.k, op.s, 0);
+        cur = {cur[0], cur[1], oh, ow};
+        break;
+      }
+      case OP_FLATTEN: {  // npu.rs:391-394
+        int64_t rest = 1;
+        for (size_t d = 1; d < cur.size(); d++) rest *= cur[d];
+        cur = {cur[0], rest};
+        break;
+      }
+      default:
+        break;
+    }
+    pl.out_shape = cur;
+    pl.out_len = numel(cur);
+  }
+  plan->out_shape = cur;
+  plan->out_len = numel(cur);
+
+  // Buffers: f32 ping-pong between ops, the last computing op writes the
+  // caller's output.
+  int last = -1;
+  for (size_t i = 0; i < nops; i++)
+    if (P->ops[i]->kind != OP_FLATTEN) last = (int)i;
+  int curbuf = BUF_INPUT;
+  for (size_t i = 0; i < nops; i++) {
+    OpPlan& pl = plan->ops[i];
+    pl.in_buf = curbuf;
+    if (P->ops[i]->kind == OP_FLATTEN) {
+      pl.out_buf = curbuf;
+    } else if ((int)i == last) {
+      pl.out_buf = BUF_OUTPUT;
+    } else {
+      pl.out_buf = curbuf == 0 ? 1 : 0;
+      plan->f32_elems = std::max(plan->f32_elems, (size_t)pl.out_len);
+    }
+    curbuf = pl.out_buf;
+  }
+
+  // Absmax slots for quantizing consumers, and producer fusion.
+  int64_t slots = 0;
+  for (size_t i = 0; i < nops; i++) {
+    const Op& op = *P->ops[i];
+    OpPlan& pl = plan->ops[i];
+    if (op.kind != OP_LINEAR && op.kind != OP_CONV) continue;
+    pl.slot_base = slots;
+    pl.slot_count = op.kind == OP_LINEAR ? 1 : pl.cs.n;
+    slots += pl.slot_count;
+    int j = (int)i - 1;
+    while (j >= 0 && P->ops[j]->kind == OP_FLATTEN) j--;
+    pl.explicit_absmax = true;
+    if (j >= 0) {
+      const int pk = P->ops[j]->kind;
+      OpPlan& prod = plan->ops[j];
+      if (op.kind == OP_LINEAR && (pk == OP_LINEAR || pk == OP_CONV || pk == OP_POOL || pk == OP_ACT)) {
+        prod.emit_slot = pl.slot_base;
+        prod.emit_per_image = 0;
+        pl.explicit_absmax = false;
+      } else if (op.kind == OP_CONV && pl.full_cov && (pk == OP_CONV || pk == OP_POOL)) {
+        prod.emit_slot = pl.slot_base;
+        prod.emit_per_image = 1;
+        pl.explicit_absmax = false;
+      }
+    }
+    size_t qb = op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len;
+    plan->q_bytes = std::max(plan->q_bytes, qb);
+  }
+  plan->n_slots = slots;
+
+  plan->f32[0].ensure(plan->f32_elems * sizeof(float));
+  plan->f32[1].ensure(plan->f32_elems * sizeof(float));
+  plan->q.ensure(plan->q_bytes);
+  plan->slots.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(uint32_t));
+  plan->scales.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(float));
+  plan->masks.ensure(std::max<size_t>(mask_host.size(), 1));
+  if (!mask_host.empty())
+    RG_HIP(hipMemcpyAsync(plan->masks.p, mask_host.data(), mask_host.size(), hipMemcpyHostToDevice, P->stream));
+  RG_HIP(hipStreamSynchronize(P->stream));
+  return plan;
+}
+
+static void ensure_capture_buffers(rgnpu_program* P, Plan& plan) {
+  if (plan.capture_ready) return;
+  const size_t n = P->ops.size();
+  plan.cap_q.resize(n);
+  plan.cap_acc.resize(n);
+  plan.cap_out.resize(n);
+  for (size_t i = 0; i < n; i++) {
+    const Op& op = *P->ops[i];
+    const OpPlan& pl = plan.ops[i];
+    plan.cap_out[i] = std::make_unique<DevBuf>();
+    plan.cap_out[i]->ensure((size_t)pl.out_len * sizeof(float));
+    if (op.kind == OP_LINEAR || op.kind == OP_CONV) {
+      plan.cap_q[i] = std::make_unique<DevBuf>();
+      plan.cap_acc[i] = std::make_unique<DevBuf>();
+      plan.cap_q[i]->ensure(op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len);
+      const size_t accn = op.kind == OP_LINEAR ? (size_t)(pl.rows * op.out_f)
+                                               : (size_t)(pl.cs.n * pl.cs.OH * pl.cs.OW * op.out_f);
+      plan.cap_acc[i]->ensure(accn * sizeof(int32_t));
+    }
+  }
+  plan.capture_ready = true;
+}
+
+static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
+  if (P->plan && (int)P->plan->in_shape.size() == ndim &&
+      std::equal(P->plan->in_shape.begin(), P->plan->in_shape.end(), shape))
+    return *P->plan;
+  P->plan.reset();
+  P->plan = make_plan(P, shape, ndim);
+  return *P->plan;
+}
+
+static void ensure_events(rgnpu_program* P) {
+  const size_t need = 2 + 4 * P->ops.size();
+  while (P->ev.size() < need) {
+    hipEvent_t e;
+    RG_HIP(hipEventCreate(&e));
+    P->ev.push_back(e);
+  }
+}
+
+// Enqueue one run; x and y are device pointers.  `ev` holds 2 + 4*ops
+// events (run start/end, then per op: op start, kernel start, kernel end,
+// op end); per-op events are recorded only when `per_op` is set.
+static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, const hipEvent_t* ev, bool per_op) {
+  hipStream_t s = P->stream;
+  const bool prof = per_op;
+  const bool cap = P->capture;
+  if (cap) ensure_capture_buffers(P, plan);
+  RG_HIP(hipEventRecord(ev[0], s));
+  uint32_t* slots = plan.slots.as<uint32_t>();
+  float* scales = plan.scales.as<float>();
+  int8_t* q = plan.q.as<int8_t>();
+  if (plan.n_slots > 0) launch_fill_u32(slots, plan.n_slots, 0u, s);
+  auto buf = [&](int id) -> float* {
+    if (id == BUF_INPUT) return const_cast<float*>(x);
+    if (id == BUF_OUTPUT) return y;
+    return plan.f32[id].as<float>();
+  };
+  for (size_t i = 0; i < P->ops.size(); i++) {
+    const Op& op = *P->ops[i];
+    const OpPlan& pl = plan.ops[i];
+    hipEvent_t ev_op0 = ev[2 + 4 * i], ev_k0 = ev[3 + 4 * i], ev_k1 = ev[4 + 4 * i], ev_op1 = ev[5 + 4 * i];
+    if (prof) RG_HIP(hipEventRecord(ev_op0, s));
+    const float* in = buf(pl.in_buf);
+    float* out = buf(pl.out_buf);
+    uint32_t* emit = pl.emit_slot >= 0 ? slots + pl.emit_slot : nullptr;
+    switch (op.kind) {
+      case OP_LINEAR: {
+        uint32_t* slot = slots + pl.slot_base;
+        if (pl.explicit_absmax) launch_absmax(in, pl.in_len, 1, slot, nullptr, nullptr, 0, 0, s);
+        launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, q, scales + pl.slot_base, s);
+        Epilogue ep;
+        ep.bias = op.d_bias.as<float>();
+        ep.act = op.act;
+        ep.act_param = op.act_param;
+        ep.absmax_in = slot;
+        ep.w_scale = op.w_scale;
+        ep.y = out;
+        ep.absmax_out = emit;
+        ep.absmax_out_per_image = 0;
+        ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
+        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        if (pl.rows > 0) {
+          if (pl.gemv)
+            launch_gemv(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+          else
+            launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, s);
+        }
+        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
+        if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
+        break;
+      }
+      case OP_CONV: {
+        const ConvShape& c = pl.cs;
+        uint32_t* sl = slots + pl.slot_base;
+        const int64_t per = c.C * c.H * c.W;
+        if (pl.explicit_absmax) {
+          const uint8_t* mk = plan.masks.as<uint8_t>() + pl.mask_off;
+          if (pl.full_cov)
+            launch_absmax(in, per, c.n, sl, nullptr, nullptr, 0, 0, s);
+          else
+            launch_absmax(in, per, c.n, sl, mk, mk + c.H, c.H, c.W, s);
+        }
+        launch_quant_images(in, per, c.n, sl, q, scales + pl.slot_base, s);
+        Epilogue ep;
+        ep.bias = op.d_bias.as<float>();
+        ep.act = op.act;
+        ep.act_param = op.act_param;
+        ep.absmax_in = sl;
+        ep.w_scale = op.w_scale;
+        ep.y = out;
+        ep.absmax_out = emit;
+        ep.absmax_out_per_image = pl.emit_per_image;
+        ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
+        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        if (c.n > 0 && c.OH * c.OW > 0) launch_conv(q, op.d_w.as<int8_t>(), c, ep, s);
+        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
+        if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)pl.in_len, hipMemcpyDeviceToDevice, s));
+        break;
+      }
+      case OP_POOL: {
+        const auto& is = pl.in_shape;
+        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        launch_maxpool(in, out, is[0], is[1], is[2], is[3], op.k, op.s, pl.out_shape[2], pl.out_shape[3], emit,
+                       pl.emit_per_image, s);
+        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
+        break;
+      }
+      case OP_FLATTEN:
+        if (prof) {
+          RG_HIP(hipEventRecord(ev_k0, s));
+          RG_HIP(hipEventRecord(ev_k1, s));
+        }
+        break;
+      case OP_ACT:
+        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        launch_activation(in, out, pl.in_len, op.act, op.act_param, emit, s);
+        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
+        break;
+      case OP_SOFTMAX: {
+        const int64_t last = pl.in_shape.back();
+        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        if (last > 0) launch_softmax(in, out, pl.in_len / last, last, s);
+        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
+        break;
+      }
+    }
+    RG_HIP(hipGetLastError());
+    if (cap)
+      RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),
+                            hipMemcpyDeviceToDevice, s));
+    if (prof) RG_HIP(hipEventRecord(ev_op1, s));
+  }
+  // A program with no computing op returns its input (Flatten only).
+  bool any = false;
+  for (auto& o : P->ops) any |= o->kind != OP_FLATTEN;
+  if (!any && plan.out_len > 0)
+    RG_HIP(hipMemcpyAsync(y, x, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToDevice, s));
+  RG_HIP(hipEventRecord(ev[1], s));
+  P->capture_valid = cap;
+}
+
+static void enqueue_profiled(rgnpu_program* P, Plan& plan, const float* x, float* y) {
+  ensure_events(P);
+  enqueue(P, plan, x, y, P->ev.data(), P->profiling > 0);
+  P->profile_pending = true;
+}
+
+static void finalize_profile(rgnpu_program* P) {
+  if (!P->profile_pending) return;
+  RG_HIP(hipEventSynchronize(P->ev[1]));
+  Plan& plan = *P->plan;
+  rgnpu_profile pr{};
+  pr.precision = RGNPU_PRECISION_INT8;
+  pr.original_layers = (int32_t)P->original_layers;
+  pr.fused_ops = (int32_t)P->ops.size();
+  pr.fp32_weight_bytes = (uint64_t)P->fp32_bytes;
+  pr.npu_weight_bytes = (uint64_t)P->npu_bytes;
+  float ms = 0.0f;
+  RG_HIP(hipEventElapsedTime(&ms, P->ev[0], P->ev[1]));
+  pr.total_ns = (uint64_t)((double)ms * 1e6);
+  P->records.assign(P->ops.size(), rgnpu_op_record{});
+  uint64_t total_macs = 0;
+  for (size_t i = 0; i < P->ops.size(); i++) {
+    rgnpu_op_record& r = P->records[i];
+    snprintf(r.op, sizeof r.op, "%s", P->ops[i]->label.c_str());
+    r.macs = plan.ops[i].macs;
+    total_macs += r.macs;
+    if (P->profiling > 0) {
+      float a = 0, b = 0;
+      RG_HIP(hipEventElapsedTime(&a, P->ev[2 + 4 * i], P->ev[5 + 4 * i]));
+      RG_HIP(hipEventElapsedTime(&b, P->ev[3 + 4 * i], P->ev[4 + 4 * i]));
+      r.ns = (uint64_t)((double)a * 1e6);
+      r.kernel_ns = (uint64_t)((double)b * 1e6);
+    }
+  }
+  pr.total_macs = total_macs;
+  pr.n_records = (int32_t)P->ops.size();
+  P->prof = pr;
+  P->have_profile = true;
+  P->profile_pending = false;
+}
+
+static void write_shape(const Plan& plan, int64_t* y_shape, int32_t* y_ndim) {
+  if (y_ndim) *y_ndim = (int32_t)plan.out_shape.size();
+  if (y_shape)
+    for (size_t d = 0; d < plan.out_shape.size(); d++) y_shape[d] = plan.out_shape[d];
+}
+
+}  // namespace rgnpu
+
+// ===================== C ABI =================================================
+#define RG_API_BEGIN try {
+#define RG_API_END                                  \
+  }                                                 \
+  catch (const rgnpu::Error& e) {                   \
+    rgnpu::g_last_error = e.what();                 \
+    return e.code;                                  \
+  }                                                 \
+  catch (const std::bad_alloc&) {                   \
+    rgnpu::g_last_error = "host allocation failed"; \
+    return RGNPU_ERR_DEVICE;                        \
+  }                                                 \
+  catch (const std::exception& e) {                 \
+    rgnpu::g_last_error = e.what();                 \
+    return RGNPU_ERR_INVALID;                       \
+  }                                                 \
+  return RGNPU_OK;
+
+extern "C" {
+
+const char* rgnpu_last_error(void) { return rgnpu::g_last_error.c_str(); }
+
+int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t precision, int32_t device,
+                         rgnpu_program** out) {
+  RG_API_BEGIN
+  if (!out) throw Error(RGNPU_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (n_layers < 0 || (n_layers > 0 && !layers)) throw Error(RGNPU_ERR_INVALID, "invalid layer list");
+  if (precision == RGNPU_PRECISION_FP16)
+    throw Error(RGNPU_ERR_UNSUPPORTED, "NpuPrecision::Fp16 is not provided by the MI355X provider");
+  if (precision != RGNPU_PRECISION_INT8) throw Error(RGNPU_ERR_INVALID, "unknown precision");
+  int count = 0;
+  RG_HIP(hipGetDeviceCount(&count));
+  if (device < 0 || device >= count) throw Error(RGNPU_ERR_DEVICE, "device index out of range");
+  auto P = std::make_unique<rgnpu_program>();
+  P->device = device;
+  RG_HIP(hipSetDevice(device));
+  RG_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
+  try {
+    compile(P.get(), layers, n_layers);
+  } catch (...) {
+    (void)hipStreamDestroy(P->stream);
+    P->stream = nullptr;
+    throw;
+  }
+  *out = P.release();
+  RG_API_END
+}
+
+void rgnpu_program_destroy(rgnpu_program* P) {
+  if (!P) return;
+  (void)hipSetDevice(P->device);
+  if (P->stream) (void)hipStreamSynchronize(P->stream);
+  P->plan.reset();
+  P->ops.clear();
+  for (auto e : P->ev) (void)hipEventDestroy(e);
+  if (P->stream) (void)hipStreamDestroy(P->stream);
+  delete P;
+}
+
+int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, int32_t ndim, float* y, int64_t y_cap,
+                      int64_t* y_shape, int32_t* y_ndim) {
+  RG_API_BEGIN
+  if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(P->mu);
+  RG_HIP(hipSetDevice(P->device));
+  Plan& plan = get_plan(P, shape, ndim);
+  write_shape(plan, y_shape, y_ndim);
+  if (!y) return RGNPU_OK;
+  if (!x && plan.in_len > 0) throw Error(RGNPU_ERR_INVALID, "x is NULL");
+  if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
+  plan.host_in.ensure((size_t)plan.in_len * sizeof(float));
+  plan.host_out.ensure((size_t)plan.out_len * sizeof(float));
+  if (plan.in_len > 0)
+    RG_HIP(hipMemcpyAsync(plan.host_in.p, x, (size_t)plan.in_len * sizeof(float), hipMemcpyHostToDevice, P->stream));
+  enqueue_profiled(P, plan, plan.host_in.as<float>(), plan.host_out.as<float>());
+  if (plan.out_len > 0)
+    RG_HIP(hipMemcpyAsync(y, plan.host_out.p, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToHost, P->stream));
+  RG_HIP(hipStreamSynchronize(P->stream));
+  finalize_profile(P);
+  RG_API_END
+}
+
+int rgnpu_program_run_device(rgnpu_program* P, const float* d_x, const int64_t* shape, int32_t ndim, float* d_y,
+                             int64_t y_cap, int64_t* y_shape, int32_t* y_ndim) {
+  RG_API_BEGIN
+  if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(P->mu);
+  RG_HIP(hipSetDevice(P->device));
+  Plan& plan = get_plan(P, shape, ndim);
+  write_shape(plan, y_shape, y_ndim);
+  if (!d_y) return RGNPU_OK;
+  if (!d_x && plan.in_len > 0) throw Error(RGNPU_ERR_INVALID, "x is NULL");
+  if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
+  enqueue_profiled(P, plan, d_x, d_y);
+  RG_API_END
+}
+
+int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* shape, int32_t ndim, float* d_y,
+                            int64_t y_cap, int32_t iters, int32_t per_kernel_events, double* total_ms,
+                            rgnpu_op_record* avg, int32_t cap) {
+  RG_API_BEGIN
+  if (!P || !shape || !d_y || iters <= 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
+  std::lock_guard<std::mutex> lk(P->mu);
+  RG_HIP(hipSetDevice(P->device));
+  Plan& plan = get_plan(P, shape, ndim);
+  if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
+  const size_t per = 2 + 4 * P->ops.size();
+  const size_t sets = per_kernel_events ? (size_t)iters : 1;
+  std::vector<hipEvent_t> evs(per * sets + 2, nullptr);
+  struct Guard {
+    std::vector<hipEvent_t>& v;
+    ~Guard() {
+      for (auto e : v)
+        if (e) (void)hipEventDestroy(e);
+    }
+  } guard{evs};
+  for (auto& e : evs) RG_HIP(hipEventCreate(&e));
+  hipEvent_t t0 = evs[per * sets], t1 = evs[per * sets + 1];
+  RG_HIP(hipStreamSynchronize(P->stream));
+  RG_HIP(hipEventRecord(t0, P->stream));
+  for (int32_t it = 0; it < iters; it++) {
+    const hipEvent_t* set = evs.data() + (per_kernel_events ? per * (size_t)it : 0);
+    enqueue(P, plan, d_x, d_y, set, per_kernel_events != 0);
+  }
+  RG_HIP(hipEventRecord(t1, P->stream));
+  RG_HIP(hipEventSynchronize(t1));
+  float ms = 0.0f;
+  RG_HIP(hipEventElapsedTime(&ms, t0, t1));
+  if (total_ms) *total_ms = ms;
+  if (avg) {
+    for (size_t i = 0; i < P->ops.size() && (int32_t)i < cap; i++) {
+      rgnpu_op_record r{};
+      snprintf(r.op, sizeof r.op, "%s", P->ops[i]->label.c_str());
+      r.macs = plan.ops[i].macs;
+      if (per_kernel_events) {
+        double a = 0, b = 0;
+        for (int32_t it = 0; it < iters; it++) {
+          const hipEvent_t* set = evs.data() + per * (size_t)it;
+          float x = 0, y = 0;
+          RG_HIP(hipEventElapsedTime(&x, set[2 + 4 * i], set[5 + 4 * i]));
+          RG_HIP(hipEventElapsedTime(&y, set[3 + 4 * i], set[4 + 4 * i]));
+          a += x;
+          b += y;
+        }
+        r.ns = (uint64_t)(a / iters * 1e6);
+        r.kernel_ns = (uint64_t)(b / iters * 1e6);
+      }
+      avg[i] = r;
+    }
+  }
+  RG_API_END
+}
+
+int rgnpu_program_synchronize(rgnpu_program* P) {
+  RG_API_BEGIN
+  if (!P) throw Error(RGNPU_ERR_INVALID, "NULL program");
+  std::lock_guard<std::mutex> lk(P->mu);
+  RG_HIP(hipSetDevice(P->device));
+  RG_HIP(hipStreamSynchronize(P->stream));
+  if (P->plan) finalize_profile(P);
+  RG_API_END
+}
+
+int rgnpu_program_set_profiling(rgnpu_program* P, int32_t level) {
+  RG_API_BEGIN
+  if (!P) throw Error(RGNPU_ERR_INVALID, "NULL program");
+  std::lock_guard<std::mutex> lk(P->mu);
+  P->profiling = level > 0 ? 1 : 0;
+  RG_API_END
+}
+
+int rgnpu_program_profile(rgnpu_program* P, rgnpu_profile* out, rgnpu_op_record* records, int32_t cap) {
+  RG_API_BEGIN
+  if (!P || !out) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(P->mu);
+  RG_HIP(hipSetDevice(P->device));
+  if (P->plan) finalize_profile(P);
+  if (!P->have_profile) throw Error(RGNPU_ERR_INVALID, "no run has completed yet");
+  *out = P->prof;
+  if (records)
+    for (int32_t i = 0; i < cap && i < (int32_t)P->records.size(); i++) records[i] = P->records[(size_t)i];
+  RG_API_END
+}
+
+int64_t rgnpu_program_num_ops(const rgnpu_program* P) { return P ? (int64_t)P->ops.size() : -1; }
+
+int64_t rgnpu_program_op_label(const rgnpu_program* P, int64_t i, char* buf, int64_t cap) {
+  if (!P || i < 0 || i >= (int64_t)P->ops.size()) return -1;
+  const std::string& l = P->ops[(size_t)i]->label;
+  if (buf && cap > 0) snprintf(buf, (size_t)cap, "%s", l.c_str());
+  return (int64_t)l.size();
+}
+
+int64_t rgnpu_program_op_weight(const rgnpu_program* P, int64_t i, int8_t* dst, int64_t cap, float* scale) {
+  if (!P || i < 0 || i >= (int64_t)P->ops.size()) return -1;
+  const Op& op = *P->ops[(size_t)i];
+  if (scale) *scale = op.w_scale;
+  if (dst) std::memcpy(dst, op.wq.data(), (size_t)std::min<int64_t>(cap, (int64_t)op.wq.size()));
+  return (int64_t)op.wq.size();
+}
+
+int64_t rgnpu_program_summary(const rgnpu_program* P, char* buf, int64_t cap) {
+  if (!P) return -1;
+  // NpuProgram::summary (npu.rs:280-293)
+  const float ratio = P->npu_bytes == 0 ? 1.0f : (float)P->fp32_bytes / (float)P->npu_bytes;
+  std::string names;
+  for (size_t i = 0; i < P->ops.size(); i++) {
+    if (i) names += " -> ";
+    names += P->ops[i]->label;
+  }
+  char head[512];
+  snprintf(head, sizeof head,
+           "InferenceSession [provider = MI355X (INT8), layers: %lld -> %zu fused ops, weights: %lld B -> %lld B (%.2fx "
+           "compression)]\n  Pipeline: ",
+           (long long)P->original_layers, P->ops.size(), (long long)P->fp32_bytes, (long long)P->npu_bytes, (double)ratio);
+  std::string s = std::string(head) + names;
+  if (buf && cap > 0) snprintf(buf, (size_t)cap, "%s", s.c_str());
+  return (int64_t)s.size();
+}
+
+int rgnpu_program_set_capture(rgnpu_program* P, int32_t on) {
+  RG_API_BEGIN
+  if (!P) throw Error(RGNPU_ERR_INVALID, "NULL program");
+  std::lock_guard<std::mutex> lk(P->mu);
+  P->capture = on != 0;
+  if (!P->capture) P->capture_valid = false;
+  RG_API_END
+}
+
+int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* dst, int64_t cap_bytes) {
+  try {
+    if (!P || !P->plan || !P->capture_valid || i < 0 || i >= (int64_t)P->ops.size()) {
+      rgnpu::g_last_error = "no capture available";
+      return -1;
+    }
+    std::lock_guard<std::mutex> lk(P->mu);
+    RG_HIP(hipSetDevice(P->device));
+    RG_HIP(hipStreamSynchronize(P->stream));
+    Plan& plan = *P->plan;
+    const Op& op = *P->ops[(size_t)i];
+    const OpPlan& pl = plan.ops[(size_t)i];
+    const bool gemm = op.kind == OP_LINEAR || op.kind == OP_CONV;
+    auto copy_out = [&](const void* src, int64_t count, size_t elem) -> int64_t {
+      if (dst) {
+        const int64_t bytes = std::min<int64_t>(cap_bytes, count * (int64_t)elem);
+        if (bytes > 0) RG_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+      }
+      return count;
+    };
+    switch (what) {
+      case RGNPU_CAP_OUT:
+        return copy_out(plan.cap_out[(size_t)i]->p, pl.out_len, sizeof(float));
+      case RGNPU_CAP_ACC: {
+        if (!gemm) return 0;
+        const int64_t n = op.kind == OP_LINEAR ? pl.rows * op.out_f : pl.cs.n * pl.cs.OH * pl.cs.OW * op.out_f;
+        return copy_out(plan.cap_acc[(size_t)i]->p, n, sizeof(int32_t));
+      }
+      case RGNPU_CAP_SCALE:
+        if (!gemm) return 0;
+        return copy_out(plan.scales.as<float>() + pl.slot_base, pl.slot_count, sizeof(float));
+      case RGNPU_CAP_QACT: {
+        if (!gemm) return 0;
+        if (op.kind == OP_LINEAR) {
+          std::vector<int8_t> full((size_t)(pl.Mpad * op.Kpad));
+          RG_HIP(hipMemcpy(full.data(), plan.cap_q[(size_t)i]->p, full.size(), hipMemcpyDeviceToHost));
+          const int64_t n = pl.rows * op.K;
+          if (dst) {
+            int8_t* d = static_cast<int8_t*>(dst);
+            for (int64_t r = 0; r < pl.rows; r++)
+              for (int64_t c = 0; c < op.K; c++) {
+                const int64_t o = r * op.K + c;
+                if (o < cap_bytes) d[o] = full[(size_t)(r * op.Kpad + c)];
+              }
+          }
+          return n;
+        }
+        // Conv: transposed im2col [n, L, C*k*k] of the quantized image.
+        const ConvShape& c = pl.cs;
+        std::vector<int8_t> img((size_t)pl.in_len);
+        RG_HIP(hipMemcpy(img.data(), plan.cap_q[(size_t)i]->p, img.size(), hipMemcpyDeviceToHost));
+        const int64_t L = c.OH * c.OW, KK = op.K;
+        const int64_t n = c.n * L * KK;
+        if (dst) {
+          int8_t* d = static_cast<int8_t*>(dst);
+          for (int64_t b = 0; b < c.n; b++)
+            for (int64_t l = 0; l < L; l++)
+              for (int64_t kk = 0; kk < KK; kk++) {
+                const int64_t o = (b * L + l) * KK + kk;
+                if (o >= cap_bytes) continue;
+                const int64_t ch = kk / (c.k * c.k), rem = kk % (c.k * c.k), ki = rem / c.k, kj = rem % c.k;
+                const int64_t iy = (l / c.OW) * c.stride + ki - c.pad, ix = (l % c.OW) * c.stride + kj - c.pad;
+                int8_t v = 0;
+                if (iy >= 0 && iy < c.H && ix >= 0 && ix < c.W) v = img[(size_t)(((b * c.C + ch) * c.H + iy) * c.W + ix)];
+                d[o] = v;
+              }
+        }
+        return n;
+      }
+    }
+    return -1;
+  } catch (const std::exception& e) {
+    rgnpu::g_last_error = e.what();
+    return -1;
+  }
+}
+
+int rgnpu_device_count(int32_t* count) {
+  RG_API_BEGIN
+  int c = 0;
+  RG_HIP(hipGetDeviceCount(&c));
+  if (count) *count = c;
+  RG_API_END
+}
+
+int rgnpu_device_alloc(int32_t device, int64_t bytes, void** out) {
+  RG_API_BEGIN
+  if (!out || bytes < 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
+  RG_HIP(hipSetDevice(device));
+  RG_HIP(hipMalloc(out, (size_t)(bytes ? bytes : 16)));
+  RG_API_END
+}
+
+int rgnpu_device_free(void* p) {
+  RG_API_BEGIN
+  if (p) RG_HIP(hipFree(p));
+  RG_API_END
+}
+
+int rgnpu_memcpy_h2d(void* dst, const void* src, int64_t bytes) {
+  RG_API_BEGIN
+  if (bytes > 0) RG_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+  RG_API_END
+}
+
+int rgnpu_memcpy_d2h(void* dst, const void* src, int64_t bytes) {
+  RG_API_BEGIN
+  if (bytes > 0) RG_HIP(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+  RG_API_END
+}
+
+int rgnpu_device_synchronize(void) {
+  RG_API_BEGIN
+  RG_HIP(hipDeviceSynchronize());
+  RG_API_END
+}
+
+}  // extern "C"

@@ -1,0 +1,77 @@
+// rgnpu_internal.h — declarations shared by the host runtime (program.cpp)
+// and the HIP kernels (kernels.hip).  Nothing here is part of the C ABI.
+#pragma once
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace rgnpu {
+
+// Padding rules for device operands.  Weights are stored [Npad, Kpad] with
+// zero rows/columns so every MFMA tile load stays in bounds.
+constexpr int64_t kRowPad = 256;   // Linear output features and activation rows
+constexpr int64_t kKPad = 128;     // reduction dimension (bytes)
+constexpr int64_t kConvOPad = 32;  // conv output channels
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Fused epilogue parameters: y = act(float(acc) * (sa * sw) + bias[n]).
+struct Epilogue {
+  const float* bias = nullptr;        // [N] (padded)
+  int act = 0;
+  float act_param = 0.0f;
+  const uint32_t* absmax_in = nullptr; // activation absmax slot(s) (sa source)
+  float w_scale = 1.0f;
+  float* y = nullptr;                  // f32 output
+  uint32_t* absmax_out = nullptr;      // nullable: absmax of y for the next op
+  int absmax_out_per_image = 0;        // conv: slot per image; else one slot
+  int32_t* acc_out = nullptr;          // nullable: i32 accumulator capture
+};
+
+// ---- launchers (kernels.hip) -------------------------------------------
+void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+
+// Absmax of x (f32) into slots[img] (atomic max of |x| bits, NaN ignored).
+// per_img elements per image, n_img images; optional coverage masks select
+// which (row, col) positions of a [C,H,W] image participate.
+void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots,
+                   const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W,
+                   hipStream_t s);
+
+// x f32 [M,K] -> q i8 [Mpad,Kpad] (zero padded), scale from slot[0].
+// scale_out (nullable) receives the scale used.
+void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad,
+                       const uint32_t* slot, int8_t* q, float* scale_out, hipStream_t s);
+
+// x f32 [n_img, per_img] -> q i8, per-image scale from slots[img].
+void launch_quant_images(const float* x, int64_t per_img, int64_t n_img, const uint32_t* slots,
+                         int8_t* q, float* scales_out, hipStream_t s);
+
+// C[M,N] = A[Mpad,Kpad] . B[Npad,Kpad]^T with the fused epilogue.
+void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad,
+                 int64_t Npad, int64_t Kpad, const Epilogue& ep, hipStream_t s);
+
+// Same contract for M <= 8 rows (weight-streaming GEMV).
+void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
+                 int64_t Kpad, const Epilogue& ep, hipStream_t s);
+
+// Implicit-GEMM conv: per image b, y[b,o,l] = act(sum_kk W[o,kk]*im2col(xq_b)[kk,l]
+// * (sa_b*sw) + bias[o]).  xq is i8 NCHW; W is [Opad, Kpad] with kk = (c*k+ki)*k+kj.
+struct ConvShape {
+  int64_t n, C, H, W, O, Opad, k, stride, pad, OH, OW, Kpad;
+};
+void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
+                 hipStream_t s);
+
+// Max pool (kernels.rs:165-213 semantics) with optional absmax of the output.
+void launch_maxpool(const float* x, float* y, int64_t n, int64_t C, int64_t H, int64_t W,
+                    int64_t k, int64_t stride, int64_t OH, int64_t OW, uint32_t* absmax_out,
+                    int absmax_per_image, hipStream_t s);
+
+// Standalone activation (in place allowed) with optional per-tensor absmax.
+void launch_activation(const float* x, float* y, int64_t n, int act, float p, uint32_t* absmax_out,
+                       hipStream_t s);
+
+// Row softmax (tensor/ops.rs:1058-1076), sequential per row.
+void launch_softmax(const float* x, float* y, int64_t outer, int64_t size, hipStream_t s);
+
+}  // namespace rgnpu

@@ -1,0 +1,243 @@
+"""GPU parity: the MI355X provider against the CPU oracle, bit for bit.
+
+Every test runs the HIP path through the C ABI (librgnpu.so) and compares,
+per fused op, the captured i8 activations, activation scale(s), i32
+accumulators and f32 outputs with the oracle's restatement of
+NpuProgram::execute (npu.rs:296-421).  The bar is bit-exact for all four,
+including f32 (the fused epilogue and activations reproduce the reference's
+f32 arithmetic and libm exactly), which is stricter than the 1e-5 relative
+tolerance the target allows; argmax equality follows.
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def make_session(rg, layers):
+    return rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+
+
+def check_against_oracle(rg, ref, layers, x, what="", parallel=True):
+    print(f"[parity] {what} x{tuple(x.shape)}", flush=True)
+    sess = make_session(rg, layers)
+    sess.set_capture(True)
+    y = sess.run(x)
+    p = ref.RefProgram(layers)
+    p.set_capture(True)
+    yr = p.run(x, parallel=parallel)
+    assert sess.op_labels() == p.labels(), what
+    assert y.shape == yr.shape, what
+    for i in range(p.num_ops):
+        for cap, name in ((0, "qact"), (1, "scale"), (2, "acc"), (3, "out")):
+            want = p.capture(i, cap)
+            if want.size == 0 and cap != 3:
+                continue
+            got = sess.capture(i, cap)
+            tag = f"{what} op{i} ({p.labels()[i]}) {name}"
+            if want.dtype == np.float32:
+                assert_bitexact_f32(got, want, tag)
+            else:
+                assert got.shape == want.shape, tag
+                if not np.array_equal(got, want):
+                    bad = np.flatnonzero(got != want)
+                    raise AssertionError(f"{tag}: {bad.size} differ, first {bad[:5]} got {got[bad[:5]]} "
+                                         f"want {want[bad[:5]]}")
+    assert_bitexact_f32(y, yr, what + " output")
+    if y.ndim == 2 and y.shape[1] > 1 and y.shape[0] > 0:
+        assert np.array_equal(np.argmax(y, 1), np.argmax(yr, 1))
+    prof = sess.last_npu_profile()
+    assert prof is not None and prof.fused_ops == p.num_ops and prof.original_layers == p.original_layers
+    assert [r.op for r in prof.records] == p.labels()
+    assert [r.macs for r in prof.records] == [p.op_macs(i) for i in range(p.num_ops)]
+    assert prof.fp32_weight_bytes == p.fp32_bytes and prof.npu_weight_bytes == p.npu_bytes
+    sess.close()
+    return y
+
+
+def test_golden_fixtures(rg, ref):
+    import golden_cases
+    for case in golden_cases.load_all():
+        print(f"[golden] {case['name']}", flush=True)
+        sess = make_session(rg, case["layers"])
+        sess.set_capture(True)
+        y = sess.run(case["x"])
+        assert sess.op_labels() == case["labels"]
+        assert_bitexact_f32(y, case["y"], case["name"])
+        for i, caps in enumerate(case["caps"]):
+            for what, arr in caps.items():
+                got = sess.capture(i, what)
+                if arr.dtype == np.float32:
+                    assert_bitexact_f32(got, arr, f"{case['name']} op{i} cap{what}")
+                else:
+                    assert np.array_equal(got, arr), f"{case['name']} op{i} cap{what}"
+        sess.close()
+
+
+def test_quickstart_mlp(rg, ref):
+    from rustgears_amd import configs
+    model, x = configs.quickstart()
+    check_against_oracle(rg, ref, model.export(), x, "quickstart")
+
+
+def test_deep_mlp_full(rg, ref):
+    from rustgears_amd import configs
+    model, x = configs.deep_mlp()
+    check_against_oracle(rg, ref, model.export(), x, "deep_mlp[4096,784]")
+
+
+def test_cnn_full(rg, ref):
+    from rustgears_amd import configs
+    model, x = configs.cnn()
+    check_against_oracle(rg, ref, model.export(), x, "cnn[256,3,32,32]")
+
+
+def test_linear_stack_gelu_scaled(rg, ref):
+    from rustgears_amd import configs
+    model, x = configs.linear_stack(rows=384, width=640, depth=4)
+    check_against_oracle(rg, ref, model.export(), x, "stack 640 gelu")
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gemv_silu_scaled(rg, ref, batch):
+    from rustgears_amd import configs
+    layers, x = configs.gemv(batch=batch, d=1024, h=3584)
+    check_against_oracle(rg, ref, layers, x, f"gemv b{batch}")
+
+
+@pytest.mark.parametrize("rows", [1, 2, 7, 8, 9, 16, 255, 256, 257])
+def test_rows_around_gemv_and_tile_boundaries(rg, ref, rows):
+    rg.manual_seed(rows)
+    from rustgears_amd import nn
+    model = nn.Sequential().add(nn.Linear(200, 130)).add(nn.Relu()).add(nn.Linear(130, 7))
+    check_against_oracle(rg, ref, model.export(), rg.randn([rows, 200]), f"rows={rows}")
+
+
+@pytest.mark.parametrize("k,n", [(1, 1), (3, 300), (64, 64), (127, 129), (1000, 5), (4100, 17)])
+def test_ragged_k_and_n(rg, ref, k, n):
+    rg.manual_seed(k * 7 + n)
+    from rustgears_amd import nn
+    model = nn.Sequential().add(nn.Linear(k, n)).add(nn.LeakyRelu(0.05))
+    check_against_oracle(rg, ref, model.export(), rg.randn([33, k]), f"k={k} n={n}")
+
+
+@pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "gelu", "leaky", "silu", "none"])
+def test_fused_activations(rg, ref, act):
+    from rustgears_amd.inference import Activation, LayerSpec
+    a = {"relu": Activation.RELU, "sigmoid": Activation.SIGMOID, "tanh": Activation.TANH, "gelu": Activation.GELU,
+         "leaky": Activation.leaky_relu(0.01), "silu": Activation.SILU, "none": Activation.NONE}[act]
+    rg.manual_seed(99)
+    w, b = rg.randn([96 * 80]), rg.randn([80])
+    layers = [LayerSpec.Linear(96, 80, w, b), LayerSpec.Activation(a), LayerSpec.Linear(80, 24, rg.randn([80 * 24]),
+                                                                                     rg.randn([24]))]
+    check_against_oracle(rg, ref, layers, (rg.randn([40, 96]) * 3).astype(np.float32), f"act {act}")
+
+
+@pytest.mark.parametrize("spec", [(3, 8, 3, 1, 1), (4, 6, 3, 2, 0), (2, 5, 1, 1, 0), (3, 4, 2, 3, 1),
+                                  (5, 7, 5, 2, 2)])
+def test_conv_variants(rg, ref, spec):
+    c, o, k, s, p = spec
+    from rustgears_amd import nn
+    rg.manual_seed(sum(spec))
+    conv = nn.Conv2d(c, o, k).stride(s).padding(p)
+    conv2 = nn.Conv2d(o, 6, 3).padding(1)
+    model = nn.Sequential().add(conv).add(nn.Relu()).add(conv2).add(nn.Tanh())
+    check_against_oracle(rg, ref, model.export(), rg.randn([5, c, 13, 11]), f"conv {spec}")
+
+
+def test_pool_and_flatten_chain(rg, ref):
+    from rustgears_amd import nn
+    rg.manual_seed(5)
+    model = (nn.Sequential().add(nn.Conv2d(2, 8, 3)).add(nn.Relu()).add(nn.MaxPool2d(3, 2)).add(nn.Conv2d(8, 4, 2))
+             .add(nn.MaxPool2d(2)).add(nn.Flatten()).add(nn.Linear(4 * 2 * 2, 5)))
+    check_against_oracle(rg, ref, model.export(), rg.randn([4, 2, 13, 13]), "pool chain")
+
+
+def test_special_values(rg, ref):
+    from rustgears_amd import nn
+    rg.manual_seed(8)
+    model = nn.Sequential().add(nn.Linear(16, 8)).add(nn.Relu()).add(nn.Linear(8, 4))
+    layers = model.export()
+    x = rg.randn([6, 16])
+    x[0, 3] = np.nan
+    x[1, :] = 0.0
+    check_against_oracle(rg, ref, layers, x, "nan row")
+    check_against_oracle(rg, ref, layers, np.zeros((3, 16), np.float32), "all zeros")
+    check_against_oracle(rg, ref, layers, np.full((2, 16), 1e-13, np.float32), "tiny (scale 1)")
+
+
+def test_standalone_ops(rg, ref):
+    from rustgears_amd.inference import Activation, LayerSpec
+    rg.manual_seed(12)
+    layers = [LayerSpec.ChannelAffine(rg.randn([10]), rg.randn([10])), LayerSpec.Activation(Activation.GELU),
+              LayerSpec.Linear(10, 6, rg.randn([60]), rg.randn([6])), LayerSpec.Softmax()]
+    check_against_oracle(rg, ref, layers, rg.randn([9, 10]), "affine/act/softmax")
+    check_against_oracle(rg, ref, [LayerSpec.Flatten()], rg.randn([2, 3, 4]), "flatten only")
+
+
+def test_activation_math_sweep_on_device(rg, ref):
+    """Standalone activation kernels over 2^22 f32 bit patterns spread over
+    all binades (every 1024th pattern, plus an offset) against host libm."""
+    from rustgears_amd.inference import Activation, LayerSpec
+    bits = (np.arange(1 << 22, dtype=np.uint64) * 1024 + 517).astype(np.uint32)
+    x = bits.view(np.float32).reshape(1 << 11, 1 << 11)
+    for a in (Activation.TANH, Activation.SIGMOID, Activation.GELU, Activation.SILU):
+        print(f"[sweep] {a}", flush=True)
+        sess = make_session(rg, [LayerSpec.Activation(a)])
+        y = sess.run(x)
+        assert_bitexact_f32(y, ref.act_apply(a.code, 0.0, x), f"sweep {a}")
+        sess.close()
+
+
+def test_shape_changes_and_errors(rg, ref):
+    from rustgears_amd import nn
+    rg.manual_seed(3)
+    layers = nn.Sequential().add(nn.Linear(12, 9)).add(nn.Relu()).export()
+    sess = make_session(rg, layers)
+    p = ref.RefProgram(layers)
+    for rows in (5, 300, 1, 5):
+        x = rg.randn([rows, 12])
+        assert_bitexact_f32(sess.run(x), p.run(x), f"rows {rows}")
+    with pytest.raises(rg.RgnpuError) as e:
+        sess.run(np.ones((2, 13), np.float32))
+    assert e.value.code == 2
+    conv = make_session(rg, nn.Sequential().add(nn.Conv2d(3, 4, 3)).export())
+    with pytest.raises(rg.RgnpuError):
+        conv.run(np.ones((1, 2, 5, 5), np.float32))
+    with pytest.raises(rg.RgnpuError):
+        conv.run(np.ones((1, 3, 2, 2), np.float32))
+
+
+def test_device_resident_run_matches_host_run(rg, ref):
+    from rustgears_amd import configs
+    model, x = configs.deep_mlp(rows=512)
+    sess = make_session(rg, model.export())
+    want = sess.run(x)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(want.nbytes)
+    for _ in range(3):
+        shape = sess.run_device(dx, x.shape, dy)
+    sess.synchronize()
+    assert shape == want.shape
+    assert_bitexact_f32(dy.download(want.shape), want)
+    sess.set_capture(False)
+    sess.set_profiling(0)
+    sess.run_device(dx, x.shape, dy)
+    sess.synchronize()
+    assert_bitexact_f32(dy.download(want.shape), want)
+    assert sess.last_npu_profile().total_time_ns > 0
+
+
+def test_compilation_report(rg, ref):
+    from rustgears_amd import nn
+    rg.manual_seed(0)
+    model = nn.Sequential().add(nn.Linear(16, 64)).add(nn.BatchNorm1d(64)).add(nn.Relu()).add(nn.Linear(64, 4))
+    sess = rg.InferenceSession.from_module(model, rg.ExecutionProvider.mi355x_int8())
+    assert sess.compilation_report() == (
+        "InferenceSession [provider = MI355X (INT8), layers: 4 -> 2 fused ops, weights: 5392 B -> 1560 B "
+        "(3.46x compression)]\n  Pipeline: NPU::FusedGemmAct(16->64, ReLU) -> NPU::Gemm(64->4)")
+    sess.run(rg.randn([32, 16]))
+    prof = sess.last_npu_profile()
+    assert prof.total_macs == 40960 and prof.compression_ratio() > 3.0
