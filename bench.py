@@ -150,7 +150,7 @@ def main():
     tops = 2 * total_macs / (ms_per_step / 1e3) / 1e12
     roof, dom = dominant_roofline(args.workload, recs, layers, x, recs)
     for r in recs:
-        print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
+        print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.duration_ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
               file=sys.stderr)
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
