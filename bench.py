@@ -35,12 +35,17 @@ PEAK_I8_TOPS = 5000.0     # MI355X dense i8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
 
 
-def build_workload(name: str, batch: int):
+def build_workload(name: str, batch: int, stack_act: str = "gelu"):
     from rustgears_amd import configs
+    from rustgears_amd.inference import Activation, LayerSpec
     if name == "linear_stack":
         model, x = configs.linear_stack()
-        return model.export(), x, {"workload": "linear_stack_4x4096_gelu", "rows": 8192, "width": 4096,
-                                   "depth": 4, "activation": "GELU", "global_batch": 8192}
+        layers = model.export()
+        if stack_act != "gelu":  # measurement aid: same GEMMs with a cheap epilogue
+            act = {"relu": Activation.RELU, "none": Activation.NONE}[stack_act]
+            layers = [LayerSpec.Activation(act) if isinstance(l, LayerSpec.Activation) else l for l in layers]
+        return layers, x, {"workload": f"linear_stack_4x4096_{stack_act}", "rows": 8192, "width": 4096,
+                           "depth": 4, "activation": stack_act.upper(), "global_batch": 8192}
     if name == "gemv":
         layers, x = configs.gemv(batch=batch)
         return layers, x, {"workload": f"gemv_8192x28672_silu_b{batch}", "batch": batch, "d": 8192, "h": 28672,
@@ -114,6 +119,8 @@ def main():
     ap.add_argument("--workload", default="linear_stack",
                     choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart"])
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1 or 8)")
+    ap.add_argument("--stack-act", default="gelu", choices=["gelu", "relu", "none"],
+                    help="activation of the linear_stack workload (gelu is the benchmark config)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -125,7 +132,7 @@ def main():
     import rustgears_amd as rg
 
     t_setup = time.perf_counter()
-    layers, x, config = build_workload(args.workload, args.batch)
+    layers, x, config = build_workload(args.workload, args.batch, args.stack_act)
     sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
     out_shape = sess.output_shape(x.shape)
     dx = rg.DeviceBuffer.from_array(x)

@@ -148,6 +148,121 @@ RG_HD float tanhf_fdlibm(float x) {
   return (jx >> 31) ? -z : z;
 }
 
+// ---------------------------------------------------------------------------
+// Branch-free forms of the same two fdlibm functions, used in the GEMM
+// epilogues.  They perform the identical sequence of f32 roundings; only the
+// control flow differs: every case of expm1f's argument reduction and
+// reconstruction is computed and the right one selected, so the 64 lanes of
+// a wave never diverge.  The reduction is shared (k = 0 and k = +-1 are the
+// general formula with t = 0 and t = +-1: t*ln2_hi is exact and
+// x - (-a) == x + a), and tanhf's two divisions 2/(t+2) and -t/(t+2) share
+// their denominator.  On the GPU the correctly rounded division is
+// computed as q0 = n*rcp(d), q = fma(fma(-d, q0, n), rcp(d), q0); the
+// exhaustive device check in tests/support/devmath_gpu_check.hip confirms
+// gelu_fast == gelu and tanhf_fast == tanhf_fdlibm for all 2^32 inputs.  On
+// the host the division is the IEEE one, so the host build of these
+// functions is compared with glibc by tests/support/devmath_host_check.cpp.
+// ---------------------------------------------------------------------------
+RG_HD float div_fast(float n, float d) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q0 = n * r;
+  const float rem = __builtin_fmaf(-d, q0, n);
+  return __builtin_fmaf(rem, r, q0);
+#else
+  return n / d;
+#endif
+}
+
+// expm1f_fdlibm restricted to the arguments tanhf passes: x in (-2, 0) and
+// x in [2, 44].  (k = 1 and the |x| >= 27 ln2 negative exit never occur.)
+RG_HD float expm1f_tanh_domain(float x) {
+  const float ln2_hi = bitsf(0x3f317180u), ln2_lo = bitsf(0x3717f7d1u), invln2 = bitsf(0x3fb8aa3bu);
+  const float Q1 = bitsf(0xbd088889u), Q2 = bitsf(0x3ad00d01u), Q3 = bitsf(0xb8a670cdu),
+              Q4 = bitsf(0x36867e54u), Q5 = bitsf(0xb457edbbu);
+  const uint32_t bx = fbits(x);
+  const uint32_t hx = bx & 0x7fffffffu;
+  const bool neg = (bx >> 31) != 0;
+  // argument reduction: k = 0 (|x| <= 0.5 ln2), -1 (|x| < 1.5 ln2, x < 0), else rounded
+  float kf = invln2 * x;
+  kf = kf + (neg ? -0.5f : 0.5f);
+  const int32_t kgen = (int32_t)kf;
+  const int32_t k = hx > 0x3eb17218u ? (hx < 0x3F851592u ? (neg ? -1 : 1) : kgen) : 0;
+  const float t = (float)k;
+  const float th = t * ln2_hi;
+  const float hi = x - th;
+  const float lo = t * ln2_lo;
+  const float xr = hi - lo;
+  const float c = (hi - xr) - lo;
+  const float hfx = 0.5f * xr;
+  const float hxs = xr * hfx;
+  float p = hxs * Q5; p = Q4 + p;
+  p = hxs * p; p = Q3 + p;
+  p = hxs * p; p = Q2 + p;
+  p = hxs * p; p = Q1 + p;
+  p = hxs * p;
+  const float r1 = 1.0f + p;
+  const float rh = r1 * hfx;
+  const float tt = 3.0f - rh;
+  const float xt = xr * tt;
+  const float den = 6.0f - xt;
+  const float num = r1 - tt;
+  const float e = hxs * div_fast(num, den);
+  // k == 0
+  const float xe = xr * e;
+  const float r0 = xr - (xe - hxs);
+  // k != 0 share e2 = x*(e-c) - c - hxs
+  const float ec = e - c;
+  float e2 = xr * ec;
+  e2 = e2 - c;
+  e2 = e2 - hxs;
+  const float em = e2 - xr;
+  // k == -1
+  const float d1 = xr - e2;
+  const float rm1 = 0.5f * d1 - 0.5f;
+  // k <= -2 or k > 56
+  const uint32_t kshift = (uint32_t)k << 23;
+  const float ylow = 1.0f - em;
+  const float rlow = bitsf(fbits(ylow) + kshift) - 1.0f;
+  // 2 <= k < 23: t = 1 - 2^-k
+  const float tk = bitsf(0x3f800000u - (0x1000000u >> (k & 31)));
+  const float rmid = bitsf(fbits(tk - em) + kshift);
+  // 23 <= k <= 56: t = 2^-k
+  const float t2 = bitsf(((uint32_t)(0x7f - k) & 0x1ffu) << 23);
+  const float yh = (xr - (e2 + t2)) + 1.0f;
+  const float rhigh = bitsf(fbits(yh) + kshift);
+  float r = k == 0 ? r0 : (k == -1 ? rm1 : ((k <= -2 || k > 56) ? rlow : (k < 23 ? rmid : rhigh)));
+  return hx < 0x33000000u ? x : r;
+}
+
+RG_HD float tanhf_fast(float x) {
+  const uint32_t jx = fbits(x), ix = jx & 0x7fffffffu;
+  const float ax = bitsf(ix);
+  const bool ge1 = ix >= 0x3f800000u;
+  const float two_ax = 2.0f * ax;
+  // |x| >= 22 selects z = 1 below; capping keeps the unused lanes in range.
+  const float arg = ge1 ? (two_ax < 44.0f ? two_ax : 44.0f) : -two_ax;
+  const float t = expm1f_tanh_domain(arg);
+  const float d = t + 2.0f;
+  const float q = div_fast(ge1 ? 2.0f : -t, d);
+  float z = ge1 ? 1.0f - q : q;
+  z = ix >= 0x41b00000u ? 1.0f : z;                // |x| >= 22 (and +-inf)
+  const float signed_z = (jx >> 31) ? -z : z;
+  const float tiny = x * (1.0f + x);               // |x| < 2^-55, and +-0
+  float r = ix < 0x24000000u ? tiny : signed_z;
+  return ix > 0x7f800000u ? x + x : r;             // NaN
+}
+
+RG_HD float gelu_fast(float x) {
+  float x3 = 0.044715f * x; x3 = x3 * x; x3 = x3 * x;
+  const float inner = x + x3;
+  const float u = 0.7978846f * inner;
+  const float t = tanhf_fast(u);
+  const float h = 0.5f * x;
+  const float one_t = 1.0f + t;
+  return h * one_t;
+}
+
 // 2^(i/32) table of ARM optimized-routines expf: asuint64(2^(i/32)) - (i<<47).
 #if defined(__HIPCC__)
 __host__ __device__
@@ -215,8 +330,8 @@ RG_HD float act_apply(int act, float p, float x) {
   switch (act) {
     case ACT_RELU: return fmax_nan_ignoring(x, 0.0f);
     case ACT_SIGMOID: return sigmoid(x);
-    case ACT_TANH: return tanhf_fdlibm(x);
-    case ACT_GELU: return gelu(x);
+    case ACT_TANH: return tanhf_fast(x);
+    case ACT_GELU: return gelu_fast(x);
     case ACT_LEAKY_RELU: return x > 0.0f ? x : p * x;
     case ACT_SILU: { float s = sigmoid(x); return x * s; }
     default: return x;

@@ -71,31 +71,19 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {
 // absmax: QuantTensor::from_f32's `fold(0, max(|v|))` (quantize.rs:19) as a
 // grid reduction.  Non-negative f32 order equals u32 bit order, so a u32
 // atomicMax of |v| bits is exact; NaN keys are dropped like f32::max does.
+// The unmasked form streams 16-byte loads; the masked form (conv inputs whose
+// rows/columns are not all read by a window) tests each element's position.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int64_t per_img,
-                                                     uint32_t* __restrict__ slots,
-                                                     const uint8_t* __restrict__ rowmask,
-                                                     const uint8_t* __restrict__ colmask, int64_t H,
-                                                     int64_t W) {
-  const int64_t img = blockIdx.y;
-  const float* xi = x + img * per_img;
-  uint32_t m = 0;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  if (rowmask) {
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per_img; e += stride) {
-      const int64_t hw = e % (H * W);
-      const int64_t iy = hw / W, ix = hw % W;
-      if (rowmask[iy] && colmask[ix]) {
-        const uint32_t k = rgmath::absmax_key(xi[e]);
-        m = k > m ? k : m;
-      }
-    }
-  } else {
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per_img; e += stride) {
-      const uint32_t k = rgmath::absmax_key(xi[e]);
-      m = k > m ? k : m;
-    }
-  }
+__device__ __forceinline__ uint32_t max4_key(float4 v, uint32_t m) {
+  uint32_t a = rgmath::absmax_key(v.x), b = rgmath::absmax_key(v.y);
+  uint32_t c = rgmath::absmax_key(v.z), d = rgmath::absmax_key(v.w);
+  a = a > b ? a : b;
+  c = c > d ? c : d;
+  a = a > c ? a : c;
+  return a > m ? a : m;
+}
+
+__device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot) {
   m = wave_max_u32(m);
   __shared__ uint32_t red[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -104,57 +92,133 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
   if (threadIdx.x == 0) {
     uint32_t r = red[0];
     for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = red[i] > r ? red[i] : r;
-    if (r) atomicMax(&slots[img], r);
+    if (r) atomicMax(slot, r);
   }
+}
+
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int64_t per_img,
+                                                     uint32_t* __restrict__ slots) {
+  const int64_t img = blockIdx.y;
+  const float* xi = x + img * per_img;
+  uint32_t m = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // 16-byte path when the image start is aligned, then the tail
+  const bool al = (reinterpret_cast<uintptr_t>(xi) & 15) == 0;
+  const int64_t n4 = al ? per_img / 4 : 0;
+  const float4* x4 = reinterpret_cast<const float4*>(xi);
+  int64_t i = tid;
+  for (; i + 3 * stride < n4; i += 4 * stride) {
+    const float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
+    m = max4_key(a, m);
+    m = max4_key(b, m);
+    m = max4_key(c, m);
+    m = max4_key(d, m);
+  }
+  for (; i < n4; i += stride) m = max4_key(x4[i], m);
+  for (int64_t e = n4 * 4 + tid; e < per_img; e += stride) {
+    const uint32_t k = rgmath::absmax_key(xi[e]);
+    m = k > m ? k : m;
+  }
+  block_max_atomic(m, &slots[img]);
+}
+
+__global__ __launch_bounds__(256) void absmax_masked_kernel(const float* __restrict__ x, int64_t per_img,
+                                                            uint32_t* __restrict__ slots,
+                                                            const uint8_t* __restrict__ rowmask,
+                                                            const uint8_t* __restrict__ colmask, int H, int W) {
+  const int64_t img = blockIdx.y;
+  const float* xi = x + img * per_img;
+  uint32_t m = 0;
+  const uint32_t hw = (uint32_t)(H * W);
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per_img; e += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t p = (uint32_t)(e % hw);
+    const uint32_t iy = p / (uint32_t)W, ix = p % (uint32_t)W;
+    if (rowmask[iy] && colmask[ix]) {
+      const uint32_t k = rgmath::absmax_key(xi[e]);
+      m = k > m ? k : m;
+    }
+  }
+  block_max_atomic(m, &slots[img]);
 }
 
 void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, const uint8_t* rowmask,
                    const uint8_t* colmask, int64_t H, int64_t W, hipStream_t s) {
   if (per_img <= 0 || n_img <= 0) return;
-  int64_t bx = (per_img + 256 * 8 - 1) / (256 * 8);
-  if (bx > 2048) bx = 2048;
+  int64_t bx = (per_img + 256 * 16 - 1) / (256 * 16);
+  const int64_t cap = n_img >= 64 ? 8 : 2048;
+  if (bx > cap) bx = cap;
   if (bx < 1) bx = 1;
-  hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots, rowmask,
-                     colmask, H, W);
+  if (rowmask)
+    hipLaunchKernelGGL(absmax_masked_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
+                       rowmask, colmask, (int)H, (int)W);
+  else
+    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots);
 }
 
 // ---------------------------------------------------------------------------
-// quantize rows: x f32 [M,K] -> q i8 [Mpad,Kpad].  One thread per 4 output
-// bytes; padding rows and columns are written as zeros.
+// quantize rows: x f32 [M,K] -> q i8 [Mpad,Kpad].  One thread per 16 output
+// bytes (one 16-byte store); padding rows and columns are written as zeros.
+// Rows whose K is a multiple of 4 are read with 16-byte loads.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d, float inv) {
+  return (uint32_t)(uint8_t)rgmath::quantize_one(a, inv) | ((uint32_t)(uint8_t)rgmath::quantize_one(b, inv) << 8) |
+         ((uint32_t)(uint8_t)rgmath::quantize_one(c, inv) << 16) |
+         ((uint32_t)(uint8_t)rgmath::quantize_one(d, inv) << 24);
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                          int64_t Mpad, int64_t Kpad, const uint32_t* __restrict__ slot,
                                                          int8_t* __restrict__ q, float* scale_out) {
   const float scale = slot_scale(slot);
   const float inv = 1.0f / scale;
-  const int64_t words_per_row = Kpad / 4;
-  const int64_t total = Mpad * words_per_row;
+  const uint32_t chunks = (uint32_t)(Kpad / 16);
+  const int64_t total = Mpad * (int64_t)chunks;
   for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = w / words_per_row;
-    const int64_t c0 = (w % words_per_row) * 4;
-    uint32_t packed = 0;
+    const int64_t r = w / chunks;
+    const uint32_t c0 = (uint32_t)(w - r * chunks) * 16u;
+    v4i out = v4i{0, 0, 0, 0};
     if (r < M) {
       const float* xr = x + r * K;
+      if (VEC && c0 + 16 <= (uint32_t)K) {
+        const float4* p = reinterpret_cast<const float4*>(xr + c0);
+        const float4 a = p[0], b = p[1], c = p[2], d = p[3];
+        out[0] = (int)pack4(a.x, a.y, a.z, a.w, inv);
+        out[1] = (int)pack4(b.x, b.y, b.z, b.w, inv);
+        out[2] = (int)pack4(c.x, c.y, c.z, c.w, inv);
+        out[3] = (int)pack4(d.x, d.y, d.z, d.w, inv);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int64_t c = c0 + e;
-        const int8_t v = c < K ? rgmath::quantize_one(xr[c], inv) : (int8_t)0;
-        packed |= (uint32_t)(uint8_t)v << (8 * e);
+        for (int g = 0; g < 4; g++) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const uint32_t c = c0 + (uint32_t)(g * 4 + e);
+            v[e] = c < (uint32_t)K ? xr[c] : 0.0f;
+          }
+          out[g] = (int)pack4(v[0], v[1], v[2], v[3], inv);
+        }
       }
     }
-    reinterpret_cast<uint32_t*>(q)[w] = packed;
+    reinterpret_cast<v4i*>(q)[w] = out;
   }
   if (scale_out && blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
 }
 
 void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad, const uint32_t* slot,
                        int8_t* q, float* scale_out, hipStream_t s) {
-  const int64_t words = Mpad * (Kpad / 4);
-  if (words <= 0) return;
-  int64_t blocks = (words + 255) / 256;
+  const int64_t chunks = Mpad * (Kpad / 16);
+  if (chunks <= 0) return;
+  int64_t blocks = (chunks + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(quant_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
-                     scale_out);
+  const bool vec = (K % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(quant_rows_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
+                       scale_out);
+  else
+    hipLaunchKernelGGL(quant_rows_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
+                       scale_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -368,54 +432,278 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__
   epilogue_tile<TM, TN, CLD, false>(Cs, tc, cs, ep);
 }
 
+// ---------------------------------------------------------------------------
+// Large-problem i8 GEMM (two workgroups per CU).
+//
+// Block tile 256 x 128, K step 64 bytes, 4 waves in a 2x2 grid, each wave
+// 128 x 64 from 8 x 4 v_mfma_i32_16x16x64_i8 blocks (128 accumulator
+// registers, so two waves fit per SIMD).  Operand tiles move global -> LDS
+// with global_load_lds_dwordx4 (no VGPR staging) through a 3-stage ring: the
+// loads for step k+2 are in flight while step k is consumed.  Each DMA
+// instruction fills 1 KiB = 16 rows x 64 bytes; lane i lands at byte 16*i,
+// so the XOR swizzle of 16-byte chunks (chunk ^ ((row >> 1) & 3)) is applied
+// by choosing which global chunk each lane fetches.  With that swizzle the
+// MFMA operand reads (16 rows, one chunk) are bank-conflict free on gfx950.
+// The stage barrier is a raw s_barrier: each wave first waits for its own
+// DMA loads (vmcnt), so no fence-induced vmcnt(0) drains the pipeline.
+//
+// Tiles are ordered so the workgroups resident on one XCD (hardware deals
+// workgroups round-robin over the 8 XCDs) cover a compact group of 8 M-tiles,
+// which keeps their A and B panels in that XCD's L2.
+// ---------------------------------------------------------------------------
+#define RG_LDS_AS __attribute__((address_space(3)))
+
+namespace big {
+constexpr int BM = 256, BN = 128, BK = 64, STAGES = 3;
+constexpr int A_ST = BM * BK, B_ST = BN * BK, ST = A_ST + B_ST;
+constexpr int SLAB_LD = 68;  // i32 words per staged epilogue row (64 + 4 pad)
+constexpr int SLAB = 16 * SLAB_LD * 4;
+constexpr int GROUP_M = 8;
+}  // namespace big
+
+__device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
+
+template <int ACT, bool CAP>
+__device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int rows, float* yp, int32_t* ap, int64_t N,
+                                                      float cs, float b, float p, int lane) {
+  uint32_t amax = 0;
+#pragma unroll 1
+  for (int r = 0; r < rows; r++) {
+    const int32_t a = slab[r * big::SLAB_LD + lane];
+    const float v = epi_value<ACT>(a, cs, b, p);
+    *yp = v;
+    yp += N;
+    if (CAP) {
+      *ap = a;
+      ap += N;
+    }
+    const uint32_t k = rgmath::absmax_key(v);
+    amax = k > amax ? k : amax;
+  }
+  return amax;
+}
+
+// Stages the wave's 128 x 64 accumulator tile through LDS 16 rows at a time
+// and stores it row-major: lane l owns column n0 + wn*64 + l, so each store
+// instruction writes 256 contiguous bytes.  The bias and scale were loaded
+// before the K loop.
+template <int ACT, bool CAP>
+__device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[8][4], int64_t m0, int64_t n0,
+                                                 int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
+                                                 int wave, int wm, int wn, int lane) {
+  int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
+  uint32_t amax = 0;
+  const int64_t col = n0 + wn * 64 + lane;
+  // Every lane stages its accumulators (the slab is shared by the wave);
+  // lanes past the last column then store nothing.
+  const bool col_ok = col < N;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
+    const int64_t row0 = m0 + wm * 128 + i * 16;
+    const int rows = col_ok ? (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16) : 0;
+    float* yp = ep.y + row0 * N + col;
+    int32_t* ap = CAP ? ep.acc_out + row0 * N + col : nullptr;
+    const uint32_t a = big_epilogue_slab<ACT, CAP>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
+    amax = a > amax ? a : amax;
+  }
+  return amax;
+}
+
+template <int ACT>
+__device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&acc)[8][4], int64_t m0, int64_t n0,
+                                                     int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
+                                                     int wave, int wm, int wn, int lane) {
+  return ep.acc_out ? big_epilogue<ACT, true>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
+                    : big_epilogue<ACT, false>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __restrict__ A,
+                                                             const int8_t* __restrict__ B, int64_t M, int64_t N,
+                                                             int64_t Kpad, int tiles_m, int tiles_n, Epilogue ep) {
+  using namespace big;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // XCD-aware, M-grouped tile order.
+  const int total = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, local = bid >> 3;
+  const int q = total >> 3, rem = total & 7;
+  const int L = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + local;
+  const int group_span = GROUP_M * tiles_n;
+  const int group = L / group_span;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int in_group = L - group * group_span;
+  const int tile_m = first_m + in_group % gsize;
+  const int tile_n = in_group / gsize;
+  const int64_t m0 = (int64_t)tile_m * BM, n0 = (int64_t)tile_n * BN;
+  // Epilogue operands are fetched now; they arrive while the K loop runs.
+  const int64_t my_col = n0 + wn * 64 + lane;
+  const float bias_v = my_col < N ? ep.bias[my_col] : 0.0f;
+  const uint32_t absmax_in_bits = *ep.absmax_in;
+
+  // DMA addressing: uniform tile base pointers plus 32-bit per-lane offsets.
+  // Wave w fills A rows [64w, 64w+64) and B rows [32w, 32w+32) of a stage.
+  const uint32_t kp = (uint32_t)Kpad;
+  const int8_t* const abase = A + m0 * Kpad;
+  const int8_t* const bbase = B + n0 * Kpad;
+  const int lr = lane >> 2, lp = lane & 3;
+  uint32_t offa[4], offb[2];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int r = wave * 64 + j * 16 + lr;
+    offa[j] = (uint32_t)r * kp + (uint32_t)((lp ^ lds_swz(r)) << 4);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int r = wave * 32 + j * 16 + lr;
+    offb[j] = (uint32_t)r * kp + (uint32_t)((lp ^ lds_swz(r)) << 4);
+  }
+  auto issue = [&](uint32_t st_off, uint32_t k0) {
+    int8_t* sa = smem + st_off;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      __builtin_amdgcn_global_load_lds(abase + (offa[j] + k0), (RG_LDS_AS void*)(sa + (wave * 64 + j * 16) * BK), 16,
+                                       0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      __builtin_amdgcn_global_load_lds(bbase + (offb[j] + k0),
+                                       (RG_LDS_AS void*)(sa + A_ST + (wave * 32 + j * 16) * BK), 16, 0, 0);
+  };
+
+  v4i acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // MFMA operand read offset: row (lane & 15) of a 16-row block, chunk lane>>4.
+  const uint32_t rd = (uint32_t)((lane & 15) * BK + (((lane >> 4) ^ lds_swz(lane & 15)) << 4));
+  const uint32_t rda = rd + (uint32_t)(wm * 128 * BK), rdb = rd + (uint32_t)(A_ST + wn * 64 * BK);
+  const int nk = (int)(Kpad / BK);
+  issue(0, 0);
+  issue(ST, nk > 1 ? BK : 0);  // two groups always in flight before the loop
+  uint32_t st_rd = 0, st_is = 2 * ST;
+  for (int kt = 0; kt < nk; kt++) {
+    // Loads of steps kt+1 (and the step issued last iteration) may stay in
+    // flight; step kt's six DMA instructions must have landed.
+    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int8_t* sa = smem + st_rd;
+    // B fragments first, then A in consumption order, so each MFMA row
+    // block waits only for its own A fragment (lgkmcnt counts in order).
+    v4i bf[4], af[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const v4i*>(sa + rdb + j * 16 * BK);
+#pragma unroll
+    for (int i = 0; i < 8; i++) af[i] = *reinterpret_cast<const v4i*>(sa + rda + i * 16 * BK);
+    // Always issue (the last two steps re-fetch step nk-1 into the stage
+    // that is free), so both control paths keep the same counter state and
+    // the MFMAs below wait for their own fragments only.
+    issue(st_is, (uint32_t)(kt + 2 < nk ? kt + 2 : nk - 1) * BK);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    st_rd = st_rd == 2 * ST ? 0 : st_rd + ST;
+    st_is = st_is == 2 * ST ? 0 : st_is + ST;
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(absmax_in_bits)) * ep.w_scale;
+  uint32_t amax = 0;
+#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
+  switch (ep.act) {
+    case rgmath::ACT_RELU: amax = RG_BIG_EPI(rgmath::ACT_RELU); break;
+    case rgmath::ACT_SIGMOID: amax = RG_BIG_EPI(rgmath::ACT_SIGMOID); break;
+    case rgmath::ACT_TANH: amax = RG_BIG_EPI(rgmath::ACT_TANH); break;
+    case rgmath::ACT_GELU: amax = RG_BIG_EPI(rgmath::ACT_GELU); break;
+    case rgmath::ACT_LEAKY_RELU: amax = RG_BIG_EPI(rgmath::ACT_LEAKY_RELU); break;
+    case rgmath::ACT_SILU: amax = RG_BIG_EPI(rgmath::ACT_SILU); break;
+    default: amax = RG_BIG_EPI(rgmath::ACT_NONE); break;
+  }
+#undef RG_BIG_EPI
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (lane == 0 && amax) atomicMax(ep.absmax_out, amax);
+  }
+}
+
 void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
+  const int64_t big_tiles = (Mpad / big::BM) * (Npad / big::BN);
+  if (big_tiles >= 256 && Mpad % big::BM == 0 && Npad % big::BN == 0 && Kpad % big::BK == 0) {
+    hipLaunchKernelGGL(gemm_i8_big_kernel, dim3((unsigned)big_tiles), dim3(256), 0, s, A, B, M, N, Kpad,
+                       (int)(Mpad / big::BM), (int)(Npad / big::BN), ep);
+    return;
+  }
   constexpr int TM = 128, TN = 128;
   dim3 grid((unsigned)(Npad / TN), (unsigned)(Mpad / TM));
   hipLaunchKernelGGL((gemm_i8_kernel<TM, TN>), grid, dim3(256), 0, s, A, B, M, N, Kpad, ep);
 }
 
 // ---------------------------------------------------------------------------
-// GEMV for M <= 8: weight streaming.  Each wave owns R consecutive output
-// features; per 1 KiB K chunk every lane loads 16 weight bytes per feature
-// (one coalesced 1 KiB read per feature) and 16 activation bytes per row,
-// and accumulates with v_dot4_i32_i8.  Lane sums are reduced at the end and
-// lane (m*R + r) finishes output (m, n+r).
+// GEMV for M <= 8: weight streaming, HBM-bound.  Each wave owns R = 4
+// consecutive output features.  Per loop trip every lane issues UNROLL x R
+// non-temporal 16-byte weight loads (UNROLL x 1 KiB coalesced per feature)
+// before consuming any, plus the matching activation bytes (cache resident),
+// and accumulates with v_dot4_i32_i8.  The MR x R lane partial sums are
+// reduced across the wave and lane (m*R + r) finishes output (m, n+r).
 // ---------------------------------------------------------------------------
 constexpr int kGemvR = 4;
-constexpr int kGemvMaxM = 8;
 
 template <int MR>
 __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                      int64_t M, int64_t N, int64_t Npad, int64_t Kpad, Epilogue ep) {
+                                                      int64_t N, int64_t Npad, int64_t Kpad, Epilogue ep) {
+  constexpr int UNROLL = MR <= 2 ? 4 : (MR <= 4 ? 2 : 1);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t nb = ((int64_t)blockIdx.x * 4 + wave) * kGemvR;
+  // Operands for the epilogue, fetched before the stream starts.
+  const int64_t my_col = nb + lane % kGemvR;
+  const float bias_v = (lane < MR * kGemvR && my_col < N) ? ep.bias[my_col] : 0.0f;
+  const uint32_t absmax_in_bits = *ep.absmax_in;
   if (nb >= Npad) return;
   int32_t acc[MR][kGemvR];
 #pragma unroll
   for (int m = 0; m < MR; m++)
 #pragma unroll
     for (int r = 0; r < kGemvR; r++) acc[m][r] = 0;
-
-  for (int64_t k = (int64_t)lane * 16; k < Kpad; k += 1024) {
-    v4i w[kGemvR];
+  const int8_t* wrow = B + nb * Kpad;
+  for (int64_t k0 = (int64_t)lane * 16; k0 < Kpad; k0 += 1024 * UNROLL) {
+    v4i w[UNROLL][kGemvR];
+    v4i x[UNROLL][MR];
 #pragma unroll
-    for (int r = 0; r < kGemvR; r++) w[r] = *reinterpret_cast<const v4i*>(B + (nb + r) * Kpad + k);
+    for (int u = 0; u < UNROLL; u++) {
+      const int64_t k = k0 + u * 1024;
+      const bool ok = k < Kpad;
 #pragma unroll
-    for (int m = 0; m < MR; m++) {
-      if (m < M) {
-        const v4i x = *reinterpret_cast<const v4i*>(A + (int64_t)m * Kpad + k);
+      for (int r = 0; r < kGemvR; r++)
+        w[u][r] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + r * Kpad + k)) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+        x[u][m] = ok ? *reinterpret_cast<const v4i*>(A + (int64_t)m * Kpad + k) : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; u++)
+#pragma unroll
+      for (int m = 0; m < MR; m++)
 #pragma unroll
         for (int r = 0; r < kGemvR; r++) {
           int32_t t = acc[m][r];
-          t = __builtin_amdgcn_sdot4(x[0], w[r][0], t, false);
-          t = __builtin_amdgcn_sdot4(x[1], w[r][1], t, false);
-          t = __builtin_amdgcn_sdot4(x[2], w[r][2], t, false);
-          t = __builtin_amdgcn_sdot4(x[3], w[r][3], t, false);
+          t = __builtin_amdgcn_sdot4(x[u][m][0], w[u][r][0], t, false);
+          t = __builtin_amdgcn_sdot4(x[u][m][1], w[u][r][1], t, false);
+          t = __builtin_amdgcn_sdot4(x[u][m][2], w[u][r][2], t, false);
+          t = __builtin_amdgcn_sdot4(x[u][m][3], w[u][r][3], t, false);
           acc[m][r] = t;
         }
-      }
-    }
   }
   // Reduce; afterwards every lane holds every sum and lane L keeps sum L.
   int32_t mine = 0;
@@ -426,20 +714,19 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__
       const int32_t t = wave_sum_i32(acc[m][r]);
       if (lane == m * kGemvR + r) mine = t;
     }
-  const int64_t m = lane / kGemvR, col = nb + lane % kGemvR;
-  const bool ok = lane < MR * kGemvR && m < M && col < N;
-  const float cs = slot_scale(ep.absmax_in) * ep.w_scale;
+  const int64_t m = lane / kGemvR, col = my_col;
+  const bool ok = lane < MR * kGemvR && col < N;
+  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(absmax_in_bits)) * ep.w_scale;
   float v = 0.0f;
   if (ok) {
-    const float b = ep.bias[col];
     switch (ep.act) {
-      case rgmath::ACT_RELU: v = epi_value<rgmath::ACT_RELU>(mine, cs, b, ep.act_param); break;
-      case rgmath::ACT_SIGMOID: v = epi_value<rgmath::ACT_SIGMOID>(mine, cs, b, ep.act_param); break;
-      case rgmath::ACT_TANH: v = epi_value<rgmath::ACT_TANH>(mine, cs, b, ep.act_param); break;
-      case rgmath::ACT_GELU: v = epi_value<rgmath::ACT_GELU>(mine, cs, b, ep.act_param); break;
-      case rgmath::ACT_LEAKY_RELU: v = epi_value<rgmath::ACT_LEAKY_RELU>(mine, cs, b, ep.act_param); break;
-      case rgmath::ACT_SILU: v = epi_value<rgmath::ACT_SILU>(mine, cs, b, ep.act_param); break;
-      default: v = epi_value<rgmath::ACT_NONE>(mine, cs, b, ep.act_param); break;
+      case rgmath::ACT_RELU: v = epi_value<rgmath::ACT_RELU>(mine, cs, bias_v, ep.act_param); break;
+      case rgmath::ACT_SIGMOID: v = epi_value<rgmath::ACT_SIGMOID>(mine, cs, bias_v, ep.act_param); break;
+      case rgmath::ACT_TANH: v = epi_value<rgmath::ACT_TANH>(mine, cs, bias_v, ep.act_param); break;
+      case rgmath::ACT_GELU: v = epi_value<rgmath::ACT_GELU>(mine, cs, bias_v, ep.act_param); break;
+      case rgmath::ACT_LEAKY_RELU: v = epi_value<rgmath::ACT_LEAKY_RELU>(mine, cs, bias_v, ep.act_param); break;
+      case rgmath::ACT_SILU: v = epi_value<rgmath::ACT_SILU>(mine, cs, bias_v, ep.act_param); break;
+      default: v = epi_value<rgmath::ACT_NONE>(mine, cs, bias_v, ep.act_param); break;
     }
     ep.y[m * N + col] = v;
     if (ep.acc_out) ep.acc_out[m * N + col] = mine;
@@ -453,9 +740,20 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
   const int64_t waves = Npad / kGemvR;
-  const int64_t blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((gemv_i8_kernel<kGemvMaxM>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Npad, Kpad,
-                     ep);
+  const unsigned blocks = (unsigned)((waves + 3) / 4);
+#define RG_GEMV(MRV) \
+  hipLaunchKernelGGL((gemv_i8_kernel<MRV>), dim3(blocks), dim3(256), 0, s, A, B, N, Npad, Kpad, ep)
+  switch (M) {
+    case 1: RG_GEMV(1); break;
+    case 2: RG_GEMV(2); break;
+    case 3: RG_GEMV(3); break;
+    case 4: RG_GEMV(4); break;
+    case 5: RG_GEMV(5); break;
+    case 6: RG_GEMV(6); break;
+    case 7: RG_GEMV(7); break;
+    default: RG_GEMV(8); break;
+  }
+#undef RG_GEMV
 }
 
 // ---------------------------------------------------------------------------

@@ -410,8 +410,10 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
                                            " is not a multiple of in_features");
         pl.rows = pl.in_len / op.in_f;
         pl.macs = (uint64_t)(pl.rows * op.in_f * op.out_f);
-        pl.Mpad = round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
         pl.gemv = pl.rows <= 8;
+        // the GEMV reads exactly `rows` activation rows; the MFMA GEMM reads
+        // whole 256-row tiles
+        pl.Mpad = pl.gemv ? (pl.rows > 0 ? pl.rows : 1) : round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
         cur.back() = op.out_f;
         break;
       }

@@ -22,8 +22,8 @@ static float libm_gelu(float x) {
 static float libm_silu(float x) { float s = libm_sigmoid(x); return x * s; }
 
 struct Count { uint64_t checked = 0, bad = 0; uint32_t first = 0; };
-enum { F_TANH, F_EXP, F_SIGMOID, F_GELU, F_SILU, NF };
-static const char* kNames[NF] = {"tanhf", "expf", "sigmoid", "gelu", "silu"};
+enum { F_TANH, F_EXP, F_SIGMOID, F_GELU, F_SILU, F_TANH_FAST, F_GELU_FAST, NF };
+static const char* kNames[NF] = {"tanhf", "expf", "sigmoid", "gelu", "silu", "tanhf_fast", "gelu_fast"};
 
 static bool same(float a, float b) {
   uint32_t x, y; memcpy(&x, &a, 4); memcpy(&y, &b, 4);
@@ -41,8 +41,10 @@ int main(int argc, char** argv) {
       for (uint64_t i = offset + (uint64_t)t * stride; i < (1ull << 32); i += (uint64_t)nt * stride) {
         const float x = rgmath::bitsf((uint32_t)i);
         const float got[NF] = {rgmath::tanhf_fdlibm(x), rgmath::expf_aor(x), rgmath::sigmoid(x), rgmath::gelu(x),
-                               rgmath::act_apply(rgmath::ACT_SILU, 0.0f, x)};
-        const float want[NF] = {tanhf(x), expf(x), libm_sigmoid(x), libm_gelu(x), libm_silu(x)};
+                               rgmath::act_apply(rgmath::ACT_SILU, 0.0f, x), rgmath::tanhf_fast(x),
+                               rgmath::gelu_fast(x)};
+        const float want[NF] = {tanhf(x), expf(x), libm_sigmoid(x), libm_gelu(x), libm_silu(x), tanhf(x),
+                                libm_gelu(x)};
         for (int f = 0; f < NF; f++) {
           Count& c = res[t][f];
           c.checked++;

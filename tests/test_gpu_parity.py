@@ -100,6 +100,30 @@ def test_linear_stack_gelu_scaled(rg, ref):
     check_against_oracle(rg, ref, model.export(), x, "stack 640 gelu")
 
 
+def test_linear_stack_gelu_full(rg, ref):
+    """The 4096^2 x 4 GELU stack at its benchmark size (8192 rows), through
+    the large-tile GEMM, bit-exact against the oracle."""
+    from rustgears_amd import configs
+    model, x = configs.linear_stack()
+    check_against_oracle(rg, ref, model.export(), x, "stack 4096 gelu full")
+
+
+def test_large_tile_gemm_ragged(rg, ref):
+    """Ragged M, N and K on the large-tile kernel (>= 256 tiles of 256x128)."""
+    from rustgears_amd import nn
+    rg.manual_seed(41)
+    model = nn.Sequential().add(nn.Linear(1000, 4000)).add(nn.Relu()).add(nn.Linear(4000, 37))
+    check_against_oracle(rg, ref, model.export(), rg.randn([4100, 1000]), "big ragged")
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gemv_silu_full(rg, ref, batch):
+    """The decode-shape GEMV config at full size (8192 -> 28672 SiLU -> 8192)."""
+    from rustgears_amd import configs
+    layers, x = configs.gemv(batch=batch)
+    check_against_oracle(rg, ref, layers, x, f"gemv full b{batch}")
+
+
 @pytest.mark.parametrize("batch", [1, 8])
 def test_gemv_silu_scaled(rg, ref, batch):
     from rustgears_amd import configs
