@@ -10,6 +10,8 @@
 // bandwidth kernel that can emit per-image absmax for the following conv.
 #include <hip/hip_runtime.h>
 
+#include <stdexcept>
+
 #include "devmath.h"
 #include "rgnpu_internal.h"
 
@@ -37,6 +39,25 @@ __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
 
 __device__ __forceinline__ float slot_scale(const uint32_t* slot) {
   return rgmath::scale_from_absmax(rgmath::bitsf(*slot));
+}
+
+// Per-tensor absmax from a spread slot: every lane folds one partial.  All
+// 64 lanes of the wave must be active.
+__device__ __forceinline__ uint32_t tensor_absmax_bits(const uint32_t* slot) {
+  static_assert(kSpread == 64, "one partial per lane");
+  return wave_max_u32(slot[(threadIdx.x & 63) * kSpreadStride]);
+}
+
+__device__ __forceinline__ float tensor_scale(const uint32_t* slot) {
+  return rgmath::scale_from_absmax(rgmath::bitsf(tensor_absmax_bits(slot)));
+}
+
+// Raise the partial of a spread slot that belongs to this wave (linear
+// wave index over the whole grid, modulo kSpread).
+__device__ __forceinline__ void spread_max(uint32_t* slot, uint32_t v) {
+  const uint32_t block = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const uint32_t part = (block * (blockDim.x >> 6) + (threadIdx.x >> 6)) & (kSpread - 1);
+  if (v) atomicMax(slot + part * kSpreadStride, v);
 }
 
 template <int ACT>
@@ -83,7 +104,9 @@ __device__ __forceinline__ uint32_t max4_key(float4 v, uint32_t m) {
   return a > m ? a : m;
 }
 
-__device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot) {
+// One atomic per block: into `slot` itself, or (spread) into the block's
+// partial of a spread slot.
+__device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot, bool spread) {
   m = wave_max_u32(m);
   __shared__ uint32_t red[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -92,12 +115,12 @@ __device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot) {
   if (threadIdx.x == 0) {
     uint32_t r = red[0];
     for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = red[i] > r ? red[i] : r;
-    if (r) atomicMax(slot, r);
+    if (r) atomicMax(spread ? slot + (blockIdx.x & (kSpread - 1)) * kSpreadStride : slot, r);
   }
 }
 
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int64_t per_img,
-                                                     uint32_t* __restrict__ slots) {
+                                                     uint32_t* __restrict__ slots, int spread) {
   const int64_t img = blockIdx.y;
   const float* xi = x + img * per_img;
   uint32_t m = 0;
@@ -120,7 +143,7 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
     const uint32_t k = rgmath::absmax_key(xi[e]);
     m = k > m ? k : m;
   }
-  block_max_atomic(m, &slots[img]);
+  block_max_atomic(m, spread ? slots : &slots[img], spread != 0);
 }
 
 __global__ __launch_bounds__(256) void absmax_masked_kernel(const float* __restrict__ x, int64_t per_img,
@@ -139,12 +162,13 @@ __global__ __launch_bounds__(256) void absmax_masked_kernel(const float* __restr
       m = k > m ? k : m;
     }
   }
-  block_max_atomic(m, &slots[img]);
+  block_max_atomic(m, &slots[img], false);
 }
 
-void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, const uint8_t* rowmask,
-                   const uint8_t* colmask, int64_t H, int64_t W, hipStream_t s) {
+void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, bool spread,
+                   const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W, hipStream_t s) {
   if (per_img <= 0 || n_img <= 0) return;
+  if (spread && (n_img != 1 || rowmask)) throw std::logic_error("spread absmax takes one unmasked tensor");
   int64_t bx = (per_img + 256 * 16 - 1) / (256 * 16);
   const int64_t cap = n_img >= 64 ? 8 : 2048;
   if (bx > cap) bx = cap;
@@ -153,7 +177,8 @@ void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slo
     hipLaunchKernelGGL(absmax_masked_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
                        rowmask, colmask, (int)H, (int)W);
   else
-    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots);
+    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
+                       spread ? 1 : 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -171,7 +196,7 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                          int64_t Mpad, int64_t Kpad, const uint32_t* __restrict__ slot,
                                                          int8_t* __restrict__ q, float* scale_out) {
-  const float scale = slot_scale(slot);
+  const float scale = tensor_scale(slot);
   const float inv = 1.0f / scale;
   const uint32_t chunks = (uint32_t)(Kpad / 16);
   const int64_t total = Mpad * (int64_t)chunks;
@@ -302,8 +327,11 @@ __device__ __forceinline__ void epilogue_tile(const int32_t* Cs, const TileCoord
   }
   if (ep.absmax_out) {
     amax = wave_max_u32(amax);
-    if ((threadIdx.x & 63) == 0 && amax)
-      atomicMax(ep.absmax_out + (CONV && ep.absmax_out_per_image ? tc.img : 0), amax);
+    if (CONV && ep.absmax_out_per_image) {
+      if ((threadIdx.x & 63) == 0 && amax) atomicMax(ep.absmax_out + tc.img, amax);
+    } else if ((threadIdx.x & 63) == 0) {
+      spread_max(ep.absmax_out, amax);
+    }
   }
 }
 
@@ -427,7 +455,7 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__
       for (int r = 0; r < 4; r++)
         Cs[(wm * WTM + i * 16 + (lane >> 4) * 4 + r) * CLD + wn * WTN + j * 16 + (lane & 15)] = acc[i][j][r];
   __syncthreads();
-  const float cs = slot_scale(ep.absmax_in) * ep.w_scale;
+  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const TileCoords tc{m0, n0, M, N, 0};
   epilogue_tile<TM, TN, CLD, false>(Cs, tc, cs, ep);
 }
@@ -546,7 +574,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
   // Epilogue operands are fetched now; they arrive while the K loop runs.
   const int64_t my_col = n0 + wn * 64 + lane;
   const float bias_v = my_col < N ? ep.bias[my_col] : 0.0f;
-  const uint32_t absmax_in_bits = *ep.absmax_in;
+  const uint32_t absmax_in_bits = tensor_absmax_bits(ep.absmax_in);
 
   // DMA addressing: uniform tile base pointers plus 32-bit per-lane offsets.
   // Wave w fills A rows [64w, 64w+64) and B rows [32w, 32w+32) of a stage.
@@ -633,7 +661,7 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
 #undef RG_BIG_EPI
   if (ep.absmax_out) {
     amax = wave_max_u32(amax);
-    if (lane == 0 && amax) atomicMax(ep.absmax_out, amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
   }
 }
 
@@ -651,109 +679,202 @@ void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// GEMV for M <= 8: weight streaming, HBM-bound.  Each wave owns R = 4
-// consecutive output features.  Per loop trip every lane issues UNROLL x R
-// non-temporal 16-byte weight loads (UNROLL x 1 KiB coalesced per feature)
-// before consuming any, plus the matching activation bytes (cache resident),
-// and accumulates with v_dot4_i32_i8.  The MR x R lane partial sums are
-// reduced across the wave and lane (m*R + r) finishes output (m, n+r).
+// GEMV for M <= 8: weight streaming, HBM-bound.
+//
+// A wave owns a group of R consecutive output features and walks all of K:
+// per loop trip each lane issues U x R non-temporal 16-byte weight loads
+// (U x 1 KiB coalesced per feature) before consuming any, plus the matching
+// activation bytes (cache resident), and accumulates with v_dot4_i32_i8.
+// The grid is persistent: it holds as many workgroups as fit on the device
+// at once and each wave strides over feature groups, so the whole weight
+// stream runs in one generation of waves with no tail.
+//
+// The MR x R partial sums are combined with a reduce-scatter butterfly:
+// at each xor step a lane keeps one half of its sums and sends the other,
+// so S sums cost S - 1 + log2(64 / S) shuffles instead of 6 S.  Afterwards
+// lane L holds sum L / (64 / S), i.e. output (m, n + r) with m * R + r =
+// L / (64 / S).
 // ---------------------------------------------------------------------------
-constexpr int kGemvR = 4;
+// Cross-lane exchange partners.  Offsets 32 and 16 use the gfx950
+// v_permlane32_swap / v_permlane16_swap (lane l <-> l ^ 32 / l ^ 16); the
+// smaller ones DPP within a 16-lane row: row_mirror (l ^ 15),
+// row_half_mirror (l ^ 7) and quad permutes (l ^ 2, l ^ 1).  Each partner
+// differs from l in bit OFF and agrees on every higher bit, which is all
+// the butterfly below needs.
+template <int OFF>
+__device__ __forceinline__ int32_t dpp_partner(int32_t v) {
+  static_assert(OFF == 8 || OFF == 4 || OFF == 2 || OFF == 1, "DPP partner offsets are 8, 4, 2, 1");
+  constexpr int ctrl = OFF == 8 ? 0x140 : OFF == 4 ? 0x141 : OFF == 2 ? 0x4E : 0xB1;
+  return __builtin_amdgcn_update_dpp(0, v, ctrl, 0xf, 0xf, false);
+}
 
-template <int MR>
-__global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                      int64_t N, int64_t Npad, int64_t Kpad, Epilogue ep) {
-  constexpr int UNROLL = MR <= 2 ? 4 : (MR <= 4 ? 2 : 1);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t nb = ((int64_t)blockIdx.x * 4 + wave) * kGemvR;
-  // Operands for the epilogue, fetched before the stream starts.
-  const int64_t my_col = nb + lane % kGemvR;
-  const float bias_v = (lane < MR * kGemvR && my_col < N) ? ep.bias[my_col] : 0.0f;
-  const uint32_t absmax_in_bits = *ep.absmax_in;
-  if (nb >= Npad) return;
-  int32_t acc[MR][kGemvR];
-#pragma unroll
-  for (int m = 0; m < MR; m++)
-#pragma unroll
-    for (int r = 0; r < kGemvR; r++) acc[m][r] = 0;
-  const int8_t* wrow = B + nb * Kpad;
-  for (int64_t k0 = (int64_t)lane * 16; k0 < Kpad; k0 += 1024 * UNROLL) {
-    v4i w[UNROLL][kGemvR];
-    v4i x[UNROLL][MR];
-#pragma unroll
-    for (int u = 0; u < UNROLL; u++) {
-      const int64_t k = k0 + u * 1024;
-      const bool ok = k < Kpad;
-#pragma unroll
-      for (int r = 0; r < kGemvR; r++)
-        w[u][r] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + r * Kpad + k)) : v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int m = 0; m < MR; m++)
-        x[u][m] = ok ? *reinterpret_cast<const v4i*>(A + (int64_t)m * Kpad + k) : v4i{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int u = 0; u < UNROLL; u++)
-#pragma unroll
-      for (int m = 0; m < MR; m++)
-#pragma unroll
-        for (int r = 0; r < kGemvR; r++) {
-          int32_t t = acc[m][r];
-          t = __builtin_amdgcn_sdot4(x[u][m][0], w[u][r][0], t, false);
-          t = __builtin_amdgcn_sdot4(x[u][m][1], w[u][r][1], t, false);
-          t = __builtin_amdgcn_sdot4(x[u][m][2], w[u][r][2], t, false);
-          t = __builtin_amdgcn_sdot4(x[u][m][3], w[u][r][3], t, false);
-          acc[m][r] = t;
-        }
+// Lanes with bit OFF clear get lo + partner's lo, the others hi + partner's hi.
+template <int OFF>
+__device__ __forceinline__ int32_t pair_combine(int32_t lo, int32_t hi, int lane) {
+  if constexpr (OFF == 32) {
+    const auto p = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+    return (int32_t)(p[0] + p[1]);
+  } else if constexpr (OFF == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
+    return (int32_t)(p[0] + p[1]);
+  } else {
+    const bool up = (lane & OFF) != 0;
+    return (up ? hi : lo) + dpp_partner<OFF>(up ? lo : hi);
   }
-  // Reduce; afterwards every lane holds every sum and lane L keeps sum L.
-  int32_t mine = 0;
+}
+
+template <int OFF>
+__device__ __forceinline__ int32_t fold(int32_t t, int lane) { return pair_combine<OFF>(t, t, lane); }
+
+// Reduce-scatter butterfly over the wave: S partial sums per lane in, one
+// finished sum out; lane l holds sum l / (64 / S).  S - 1 exchanges while
+// the sums halve, then log2(64 / S) folds of the last one.
+template <int S>
+__device__ __forceinline__ int32_t wave_reduce_scatter(int32_t (&v)[S], int lane) {
+  static_assert(S >= 1 && S <= 64 && (S & (S - 1)) == 0, "S must be a power of two <= 64");
+#define RG_RS_STEP(OFF, DIV)                                                  \
+  if constexpr (S >= DIV) {                                                   \
+    _Pragma("unroll") for (int i = 0; i < S / DIV; i++)                       \
+      v[i] = pair_combine<OFF>(v[i], v[i + S / DIV], lane);                   \
+  }
+  RG_RS_STEP(32, 2)
+  RG_RS_STEP(16, 4)
+  RG_RS_STEP(8, 8)
+  RG_RS_STEP(4, 16)
+  RG_RS_STEP(2, 32)
+  RG_RS_STEP(1, 64)
+#undef RG_RS_STEP
+  int32_t t = v[0];
+  if constexpr (S < 2) t = fold<32>(t, lane);
+  if constexpr (S < 4) t = fold<16>(t, lane);
+  if constexpr (S < 8) t = fold<8>(t, lane);
+  if constexpr (S < 16) t = fold<4>(t, lane);
+  if constexpr (S < 32) t = fold<2>(t, lane);
+  if constexpr (S < 64) t = fold<1>(t, lane);
+  return t;
+}
+
+constexpr int pow2_at_least(int v) { return v <= 1 ? 1 : 2 * pow2_at_least((v + 1) / 2); }
+
+template <int MR, int R, int U>
+__global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                      int64_t N, int64_t groups, int64_t Kpad, Epilogue ep) {
+  constexpr int S = pow2_at_least(MR * R);
+  constexpr int SPREAD = 64 / S;  // lanes holding the same finished sum
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  const int sidx = lane / SPREAD;
+  const int om = sidx / R, orr = sidx % R;
+  const bool owner = (lane % SPREAD) == 0 && sidx < MR * R;
+  // Uniform trip count; past the end of K a lane re-reads the last chunk
+  // (in bounds, cache resident) and pairs it with zero activations.
+  const int64_t ntrip = (Kpad + 1024 * U - 1) / (1024 * U);
+  const int64_t klast = Kpad - 16;
+  uint32_t amax = 0;
+  for (int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); g < groups; g += waves) {
+    const int64_t nb = g * R;
+    const int64_t col = nb + orr;
+    // Loaded and consumed by every lane (clamped column): a masked load would
+    // leave its register pending on the skip path and force a full memory
+    // wait at the next group.
+    const float bias_v = ep.bias[col < N ? col : N - 1];
+    int32_t acc[S];
 #pragma unroll
-  for (int m = 0; m < MR; m++)
+    for (int i = 0; i < S; i++) acc[i] = 0;
+    const int8_t* wrow = B + nb * Kpad;
+    for (int64_t t = 0; t < ntrip; t++) {
+      v4i w[U][R];
+      v4i x[U][MR];
+      bool ok[U];
 #pragma unroll
-    for (int r = 0; r < kGemvR; r++) {
-      const int32_t t = wave_sum_i32(acc[m][r]);
-      if (lane == m * kGemvR + r) mine = t;
+      for (int u = 0; u < U; u++) {
+        const int64_t k = (t * U + u) * 1024 + lane * 16;
+        ok[u] = k < Kpad;
+        const int64_t kk = ok[u] ? k : klast;
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + r * Kpad + kk));
+#pragma unroll
+        for (int m = 0; m < MR; m++) x[u][m] = *reinterpret_cast<const v4i*>(A + (int64_t)m * Kpad + kk);
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+          const v4i xv = ok[u] ? x[u][m] : v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            int32_t a = acc[m * R + r];
+            a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
+            a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
+            a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
+            a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+            acc[m * R + r] = a;
+          }
+        }
     }
-  const int64_t m = lane / kGemvR, col = my_col;
-  const bool ok = lane < MR * kGemvR && col < N;
-  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(absmax_in_bits)) * ep.w_scale;
-  float v = 0.0f;
-  if (ok) {
-    switch (ep.act) {
-      case rgmath::ACT_RELU: v = epi_value<rgmath::ACT_RELU>(mine, cs, bias_v, ep.act_param); break;
-      case rgmath::ACT_SIGMOID: v = epi_value<rgmath::ACT_SIGMOID>(mine, cs, bias_v, ep.act_param); break;
-      case rgmath::ACT_TANH: v = epi_value<rgmath::ACT_TANH>(mine, cs, bias_v, ep.act_param); break;
-      case rgmath::ACT_GELU: v = epi_value<rgmath::ACT_GELU>(mine, cs, bias_v, ep.act_param); break;
-      case rgmath::ACT_LEAKY_RELU: v = epi_value<rgmath::ACT_LEAKY_RELU>(mine, cs, bias_v, ep.act_param); break;
-      case rgmath::ACT_SILU: v = epi_value<rgmath::ACT_SILU>(mine, cs, bias_v, ep.act_param); break;
-      default: v = epi_value<rgmath::ACT_NONE>(mine, cs, bias_v, ep.act_param); break;
+    const int32_t mine = wave_reduce_scatter<S>(acc, lane);
+    // (acc as f32) * cs + bias with separate roundings, as in epi_value.
+    const float prod = (float)mine * cs;
+    const float pre = prod + bias_v;
+    if (owner && col < N) {
+      float v;
+      switch (ep.act) {
+        case rgmath::ACT_RELU: v = act_fixed<rgmath::ACT_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SIGMOID: v = act_fixed<rgmath::ACT_SIGMOID>(pre, ep.act_param); break;
+        case rgmath::ACT_TANH: v = act_fixed<rgmath::ACT_TANH>(pre, ep.act_param); break;
+        case rgmath::ACT_GELU: v = act_fixed<rgmath::ACT_GELU>(pre, ep.act_param); break;
+        case rgmath::ACT_LEAKY_RELU: v = act_fixed<rgmath::ACT_LEAKY_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SILU: v = act_fixed<rgmath::ACT_SILU>(pre, ep.act_param); break;
+        default: v = pre; break;
+      }
+      ep.y[om * N + col] = v;
+      if (ep.acc_out) ep.acc_out[om * N + col] = mine;
+      const uint32_t key = rgmath::absmax_key(v);
+      amax = key > amax ? key : amax;
     }
-    ep.y[m * N + col] = v;
-    if (ep.acc_out) ep.acc_out[m * N + col] = mine;
   }
   if (ep.absmax_out) {
-    const uint32_t amax = wave_max_u32(ok ? rgmath::absmax_key(v) : 0u);
-    if (lane == 0 && amax) atomicMax(ep.absmax_out, amax);
+    amax = wave_max_u32(amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
   }
+}
+
+// Workgroups of 256 threads of `fn` that are resident on the device at once.
+static int64_t resident_blocks(const void* fn) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
+  return (int64_t)per_cu * cus;
+}
+
+template <int MR, int R, int U>
+void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, int64_t Kpad, const Epilogue& ep,
+                   hipStream_t s, int64_t max_blocks) {
+  const void* fn = reinterpret_cast<const void*>(&gemv_i8_kernel<MR, R, U>);
+  static const int64_t cap = resident_blocks(fn);
+  const int64_t groups = Npad / R;  // Npad is a multiple of 256, so of every R used
+  int64_t blocks = (groups + 3) / 4;
+  const int64_t lim = max_blocks > 0 ? max_blocks : cap;
+  if (blocks > lim) blocks = lim;
+  hipLaunchKernelGGL((gemv_i8_kernel<MR, R, U>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
 }
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
-  const int64_t waves = Npad / kGemvR;
-  const unsigned blocks = (unsigned)((waves + 3) / 4);
-#define RG_GEMV(MRV) \
-  hipLaunchKernelGGL((gemv_i8_kernel<MRV>), dim3(blocks), dim3(256), 0, s, A, B, N, Npad, Kpad, ep)
   switch (M) {
-    case 1: RG_GEMV(1); break;
-    case 2: RG_GEMV(2); break;
-    case 3: RG_GEMV(3); break;
-    case 4: RG_GEMV(4); break;
-    case 5: RG_GEMV(5); break;
-    case 6: RG_GEMV(6); break;
-    case 7: RG_GEMV(7); break;
-    default: RG_GEMV(8); break;
+    case 1: launch_gemv_t<1, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 2: launch_gemv_t<2, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 3: launch_gemv_t<3, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 4: launch_gemv_t<4, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 5: launch_gemv_t<5, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 6: launch_gemv_t<6, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 7: launch_gemv_t<7, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    default: launch_gemv_t<8, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
   }
-#undef RG_GEMV
 }
 
 // ---------------------------------------------------------------------------
@@ -889,7 +1010,11 @@ __global__ __launch_bounds__(256) void maxpool_kernel(const float* __restrict__ 
   }
   if (absmax_out) {
     amax = wave_max_u32(amax);
-    if ((threadIdx.x & 63) == 0 && amax) atomicMax(absmax_out + (per_image ? b : 0), amax);
+    if (per_image) {
+      if ((threadIdx.x & 63) == 0 && amax) atomicMax(absmax_out + b, amax);
+    } else if ((threadIdx.x & 63) == 0) {
+      spread_max(absmax_out, amax);
+    }
   }
 }
 
@@ -933,7 +1058,7 @@ __global__ __launch_bounds__(256) void activation_kernel(const float* __restrict
   }
   if (absmax_out) {
     amax = wave_max_u32(amax);
-    if ((threadIdx.x & 63) == 0 && amax) atomicMax(absmax_out, amax);
+    if ((threadIdx.x & 63) == 0) spread_max(absmax_out, amax);
   }
 }
 

@@ -115,7 +115,8 @@ struct OpPlan {
   ConvShape cs{};
   bool full_cov = true;
   int64_t mask_off = 0;       // offset of row/col coverage masks in Plan::masks
-  int64_t slot_base = -1, slot_count = 0;
+  int64_t slot_base = -1, slot_count = 0;  // slot words offset; scales this op quantizes with
+  int64_t scale_base = -1;                  // index of its first scale in Plan::scales
   bool explicit_absmax = true;
   int64_t emit_slot = -1;     // this op's kernel writes absmax into slots[emit_slot..]
   int emit_per_image = 0;
@@ -476,15 +477,24 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     curbuf = pl.out_buf;
   }
 
-  // Absmax slots for quantizing consumers, and producer fusion.
-  int64_t slots = 0;
+  // Absmax slots for quantizing consumers, and producer fusion.  A Linear
+  // consumer gets a spread per-tensor slot (kTensorSlotWords words, 128-byte
+  // aligned), a conv consumer one word per image.
+  int64_t slots = 0, n_scales = 0;
   for (size_t i = 0; i < nops; i++) {
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR && op.kind != OP_CONV) continue;
-    pl.slot_base = slots;
     pl.slot_count = op.kind == OP_LINEAR ? 1 : pl.cs.n;
-    slots += pl.slot_count;
+    if (op.kind == OP_LINEAR) {
+      pl.slot_base = round_up(slots, kSpreadStride);
+      slots = pl.slot_base + kTensorSlotWords;
+    } else {
+      pl.slot_base = slots;
+      slots += pl.slot_count;
+    }
+    pl.scale_base = n_scales;
+    n_scales += pl.slot_count;
     int j = (int)i - 1;
     while (j >= 0 && P->ops[j]->kind == OP_FLATTEN) j--;
     pl.explicit_absmax = true;
@@ -510,7 +520,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
   plan->q.ensure(plan->q_bytes);
   plan->slots.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(uint32_t));
-  plan->scales.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(float));
+  plan->scales.ensure((size_t)std::max<int64_t>(n_scales, 1) * sizeof(float));
   plan->masks.ensure(std::max<size_t>(mask_host.size(), 1));
   if (!mask_host.empty())
     RG_HIP(hipMemcpyAsync(plan->masks.p, mask_host.data(), mask_host.size(), hipMemcpyHostToDevice, P->stream));
@@ -588,8 +598,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
     switch (op.kind) {
       case OP_LINEAR: {
         uint32_t* slot = slots + pl.slot_base;
-        if (pl.explicit_absmax) launch_absmax(in, pl.in_len, 1, slot, nullptr, nullptr, 0, 0, s);
-        launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, q, scales + pl.slot_base, s);
+        if (pl.explicit_absmax) launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s);
+        launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, q, scales + pl.scale_base, s);
         Epilogue ep;
         ep.bias = op.d_bias.as<float>();
         ep.act = op.act;
@@ -618,11 +628,11 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
         if (pl.explicit_absmax) {
           const uint8_t* mk = plan.masks.as<uint8_t>() + pl.mask_off;
           if (pl.full_cov)
-            launch_absmax(in, per, c.n, sl, nullptr, nullptr, 0, 0, s);
+            launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s);
           else
-            launch_absmax(in, per, c.n, sl, mk, mk + c.H, c.H, c.W, s);
+            launch_absmax(in, per, c.n, sl, false, mk, mk + c.H, c.H, c.W, s);
         }
-        launch_quant_images(in, per, c.n, sl, q, scales + pl.slot_base, s);
+        launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
         Epilogue ep;
         ep.bias = op.d_bias.as<float>();
         ep.act = op.act;
@@ -990,7 +1000,7 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
       }
       case RGNPU_CAP_SCALE:
         if (!gemm) return 0;
-        return copy_out(plan.scales.as<float>() + pl.slot_base, pl.slot_count, sizeof(float));
+        return copy_out(plan.scales.as<float>() + pl.scale_base, pl.slot_count, sizeof(float));
       case RGNPU_CAP_QACT: {
         if (!gemm) return 0;
         if (op.kind == OP_LINEAR) {

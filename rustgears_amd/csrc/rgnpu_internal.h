@@ -14,30 +14,43 @@ constexpr int64_t kConvOPad = 32;  // conv output channels
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Absmax slots.  A per-image absmax (conv consumers) is one u32 per image.
+// A per-tensor absmax (Linear consumers) is spread over kSpread partial
+// maxima kSpreadStride words (128 bytes) apart: each producing wave or
+// block raises the partial picked by its index, and consumers fold all
+// kSpread partials with one load per lane.  Device-scope atomics on one
+// address are serialised at the memory side on MI355X (the eight XCD L2s
+// are not coherent), so thousands of waves ending together on a single
+// slot would cost tens of microseconds.
+constexpr int kSpread = 64;
+constexpr int kSpreadStride = 32;
+constexpr int64_t kTensorSlotWords = (int64_t)kSpread * kSpreadStride;
+
 // Fused epilogue parameters: y = act(float(acc) * (sa * sw) + bias[n]).
 struct Epilogue {
   const float* bias = nullptr;        // [N] (padded)
   int act = 0;
   float act_param = 0.0f;
-  const uint32_t* absmax_in = nullptr; // activation absmax slot(s) (sa source)
+  const uint32_t* absmax_in = nullptr; // activation absmax: spread slot (Linear) or per image (conv)
   float w_scale = 1.0f;
   float* y = nullptr;                  // f32 output
   uint32_t* absmax_out = nullptr;      // nullable: absmax of y for the next op
-  int absmax_out_per_image = 0;        // conv: slot per image; else one slot
+  int absmax_out_per_image = 0;        // 1: slot per image; 0: spread per-tensor slot
   int32_t* acc_out = nullptr;          // nullable: i32 accumulator capture
 };
 
 // ---- launchers (kernels.hip) -------------------------------------------
 void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 
-// Absmax of x (f32) into slots[img] (atomic max of |x| bits, NaN ignored).
+// Absmax of x (f32) (atomic max of |x| bits, NaN ignored): per image into
+// slots[img], or with n_img == 1 and `spread` into a spread per-tensor slot.
 // per_img elements per image, n_img images; optional coverage masks select
 // which (row, col) positions of a [C,H,W] image participate.
-void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots,
+void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, bool spread,
                    const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W,
                    hipStream_t s);
 
-// x f32 [M,K] -> q i8 [Mpad,Kpad] (zero padded), scale from slot[0].
+// x f32 [M,K] -> q i8 [Mpad,Kpad] (zero padded), scale from a spread slot.
 // scale_out (nullable) receives the scale used.
 void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad,
                        const uint32_t* slot, int8_t* q, float* scale_out, hipStream_t s);
