@@ -59,10 +59,35 @@ def build_workload(name: str, batch: int, stack_act: str = "gelu"):
     if name == "quickstart":
         model, x = configs.quickstart()
         return model.export(), x, {"workload": "quickstart_mlp", "rows": 64, "global_batch": 64}
+    if name == "copy":
+        # calibration: one standalone Activation(None) = a plain f32 copy of
+        # 8192 x 4096 (128 MiB read, 128 MiB written) through the product's
+        # elementwise kernel; used to scale the FETCH_SIZE / WRITE_SIZE counters
+        from rustgears_amd import rng
+        rng.manual_seed(11)
+        x = rng.randn([8192, 4096])
+        return [LayerSpec.Activation(Activation.NONE)], x, {"workload": "copy_8192x4096_f32", "rows": 8192,
+                                                            "global_batch": 8192}
     raise SystemExit(f"unknown workload {name}")
 
 
-def dominant_roofline(name, records, layers, x, steps_records):
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` in `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.txt:
+    lines `workload<TAB>kernel label<TAB>bytes`, already scaled by the copy
+    calibration); None when that pair was not profiled."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.rstrip("\n").split("\t")
+            if len(parts) == 3 and parts[0] == workload and parts[1] == kernel:
+                return int(parts[2])
+    return None
+
+
+def dominant_roofline(name, records, layers, x, workload):
     """Roofline of the dominant kernel (largest total kernel time per step)."""
     best = max(range(len(records)), key=lambda i: records[i].kernel_ns)
     r = records[best]
@@ -79,12 +104,19 @@ def dominant_roofline(name, records, layers, x, steps_records):
         byts = li.in_features * li.out_features + 4 * li.out_features + b * li.in_features + 4 * b * li.out_features
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None, "kernel": r.op,
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
+                "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
+    if r.macs == 0:
+        # elementwise op (copy calibration): f32 in + f32 out
+        byts = 8 * int(np.prod(x.shape))
+        ach = byts / secs / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
                 "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     ops = 2 * r.macs
     ach = ops / secs / 1e12
     return {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
-            "frac": round(ach / PEAK_I8_TOPS, 4), "traffic": None, "kernel": r.op,
+            "frac": round(ach / PEAK_I8_TOPS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 
@@ -117,7 +149,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="linear_stack",
-                    choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart"])
+                    choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart", "copy"])
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1 or 8)")
     ap.add_argument("--stack-act", default="gelu", choices=["gelu", "relu", "none"],
                     help="activation of the linear_stack workload (gelu is the benchmark config)")
@@ -155,7 +187,7 @@ def main():
     value = batch / (ms_per_step / 1e3)
     total_macs = sum(r.macs for r in recs)
     tops = 2 * total_macs / (ms_per_step / 1e3) / 1e12
-    roof, dom = dominant_roofline(args.workload, recs, layers, x, recs)
+    roof, dom = dominant_roofline(args.workload, recs, layers, x, config["workload"])
     for r in recs:
         print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.duration_ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
               file=sys.stderr)

@@ -41,11 +41,15 @@ __device__ __forceinline__ float slot_scale(const uint32_t* slot) {
   return rgmath::scale_from_absmax(rgmath::bitsf(*slot));
 }
 
-// Per-tensor absmax from a spread slot: every lane folds one partial.  All
-// 64 lanes of the wave must be active.
-__device__ __forceinline__ uint32_t tensor_absmax_bits(const uint32_t* slot) {
+// Per-tensor absmax from a spread slot: every lane loads one partial and the
+// wave folds them.  All 64 lanes of the wave must be active for the fold.
+__device__ __forceinline__ uint32_t tensor_absmax_part(const uint32_t* slot) {
   static_assert(kSpread == 64, "one partial per lane");
-  return wave_max_u32(slot[(threadIdx.x & 63) * kSpreadStride]);
+  return slot[(threadIdx.x & 63) * kSpreadStride];
+}
+
+__device__ __forceinline__ uint32_t tensor_absmax_bits(const uint32_t* slot) {
+  return wave_max_u32(tensor_absmax_part(slot));
 }
 
 __device__ __forceinline__ float tensor_scale(const uint32_t* slot) {
@@ -461,33 +465,53 @@ __global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Large-problem i8 GEMM (two workgroups per CU).
+// Large-problem i8 GEMM.
 //
-// Block tile 256 x 128, K step 64 bytes, 4 waves in a 2x2 grid, each wave
-// 128 x 64 from 8 x 4 v_mfma_i32_16x16x64_i8 blocks (128 accumulator
-// registers, so two waves fit per SIMD).  Operand tiles move global -> LDS
-// with global_load_lds_dwordx4 (no VGPR staging) through a 3-stage ring: the
-// loads for step k+2 are in flight while step k is consumed.  Each DMA
-// instruction fills 1 KiB = 16 rows x 64 bytes; lane i lands at byte 16*i,
-// so the XOR swizzle of 16-byte chunks (chunk ^ ((row >> 1) & 3)) is applied
-// by choosing which global chunk each lane fetches.  With that swizzle the
-// MFMA operand reads (16 rows, one chunk) are bank-conflict free on gfx950.
-// The stage barrier is a raw s_barrier: each wave first waits for its own
-// DMA loads (vmcnt), so no fence-induced vmcnt(0) drains the pipeline.
+// Every wave owns a 128 x 64 output tile built from 8 x 4
+// v_mfma_i32_16x16x64_i8 blocks (128 accumulator registers, two waves per
+// SIMD).  A block tile is BM x BN from WAVES_M x WAVES_N waves, K step 64
+// bytes.  Two shapes are used: 256 x 128 (4 waves, two workgroups per CU)
+// and 256 x 256 (8 waves, one workgroup per CU), which moves a third fewer
+// operand bytes per MAC and leaves LDS for a deeper ring.
+//
+// Operand tiles move global -> LDS with global_load_lds_dwordx4 (no VGPR
+// staging) through a STAGES-deep ring: the loads for steps k+1 .. k+STAGES-1
+// are in flight while step k is consumed.  Each DMA instruction fills 1 KiB
+// = 16 rows x 64 bytes; lane i lands at byte 16*i, so the XOR swizzle of
+// 16-byte chunks (chunk ^ ((row >> 1) & 3)) is applied by choosing which
+// global chunk each lane fetches.  With that swizzle the MFMA operand reads
+// (16 rows, one chunk) are bank-conflict free on gfx950.  The stage barrier
+// is a raw s_barrier: each wave first waits for its own DMA loads (vmcnt),
+// so no fence-induced vmcnt(0) drains the pipeline.
 //
 // Tiles are ordered so the workgroups resident on one XCD (hardware deals
-// workgroups round-robin over the 8 XCDs) cover a compact group of 8 M-tiles,
-// which keeps their A and B panels in that XCD's L2.
+// workgroups round-robin over the 8 XCDs) cover a compact group of GROUP_M
+// M-tiles, which keeps their A and B panels in that XCD's L2.
 // ---------------------------------------------------------------------------
 #define RG_LDS_AS __attribute__((address_space(3)))
 
 namespace big {
-constexpr int BM = 256, BN = 128, BK = 64, STAGES = 3;
-constexpr int A_ST = BM * BK, B_ST = BN * BK, ST = A_ST + B_ST;
+constexpr int BK = 64;
 constexpr int SLAB_LD = 68;  // i32 words per staged epilogue row (64 + 4 pad)
 constexpr int SLAB = 16 * SLAB_LD * 4;
 constexpr int GROUP_M = 8;
 }  // namespace big
+
+// One global_load_lds_dwordx4: 16 bytes per lane, lane i lands at lds + 16 i
+// (the LDS address is wave-uniform).  Kept out of the kernel templates: the
+// LDS address-space cast does not survive the host compilation pass of a
+// template body, which would silently drop the kernel's host stub.
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, (RG_LDS_AS void*)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) for a compile-time N (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt and lgkmcnt left at their no-wait maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 __device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
@@ -549,13 +573,21 @@ __device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&a
                     : big_epilogue<ACT, false>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
 }
 
-__global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __restrict__ A,
-                                                             const int8_t* __restrict__ B, int64_t M, int64_t N,
-                                                             int64_t Kpad, int tiles_m, int tiles_n, Epilogue ep) {
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kernel(
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int64_t M, int64_t N, int64_t Kpad, int tiles_m,
+    int tiles_n, Epilogue ep) {
   using namespace big;
+  constexpr int NW = WAVES_M * WAVES_N;
+  static_assert(BM == 128 * WAVES_M && BN == 64 * WAVES_N, "wave tile is 128 x 64");
+  constexpr int IA = BM / 16 / NW, IB = BN / 16 / NW;  // DMA instructions per wave per stage
+  static_assert(IA * 16 * NW == BM && IB * 16 * NW == BN && IA >= 1 && IB >= 1, "DMA split");
+  static_assert(STAGES >= 3, "ring depth");
+  constexpr int A_ST = BM * BK, ST = (BM + BN) * BK;
+  static_assert(NW * SLAB <= STAGES * ST, "epilogue slabs reuse the ring");
   __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // XCD-aware, M-grouped tile order.
   const int total = tiles_m * tiles_n;
@@ -574,35 +606,33 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
   // Epilogue operands are fetched now; they arrive while the K loop runs.
   const int64_t my_col = n0 + wn * 64 + lane;
   const float bias_v = my_col < N ? ep.bias[my_col] : 0.0f;
-  const uint32_t absmax_in_bits = tensor_absmax_bits(ep.absmax_in);
+  // Partial of the input absmax; folded after the K loop so the fold does not
+  // wait on the prologue DMA.
+  const uint32_t absmax_part = tensor_absmax_part(ep.absmax_in);
 
   // DMA addressing: uniform tile base pointers plus 32-bit per-lane offsets.
-  // Wave w fills A rows [64w, 64w+64) and B rows [32w, 32w+32) of a stage.
+  // Wave w fills A rows [16 IA w, 16 IA (w+1)) and B rows [16 IB w, ...).
   const uint32_t kp = (uint32_t)Kpad;
   const int8_t* const abase = A + m0 * Kpad;
   const int8_t* const bbase = B + n0 * Kpad;
   const int lr = lane >> 2, lp = lane & 3;
-  uint32_t offa[4], offb[2];
+  uint32_t offa[IA], offb[IB];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int r = wave * 64 + j * 16 + lr;
+  for (int j = 0; j < IA; j++) {
+    const int r = (wave * IA + j) * 16 + lr;
     offa[j] = (uint32_t)r * kp + (uint32_t)((lp ^ lds_swz(r)) << 4);
   }
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int r = wave * 32 + j * 16 + lr;
+  for (int j = 0; j < IB; j++) {
+    const int r = (wave * IB + j) * 16 + lr;
     offb[j] = (uint32_t)r * kp + (uint32_t)((lp ^ lds_swz(r)) << 4);
   }
   auto issue = [&](uint32_t st_off, uint32_t k0) {
     int8_t* sa = smem + st_off;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      __builtin_amdgcn_global_load_lds(abase + (offa[j] + k0), (RG_LDS_AS void*)(sa + (wave * 64 + j * 16) * BK), 16,
-                                       0, 0);
+    for (int j = 0; j < IA; j++) dma16(abase + (offa[j] + k0), sa + (wave * IA + j) * 16 * BK);
 #pragma unroll
-    for (int j = 0; j < 2; j++)
-      __builtin_amdgcn_global_load_lds(bbase + (offb[j] + k0),
-                                       (RG_LDS_AS void*)(sa + A_ST + (wave * 32 + j * 16) * BK), 16, 0, 0);
+    for (int j = 0; j < IB; j++) dma16(bbase + (offb[j] + k0), sa + A_ST + (wave * IB + j) * 16 * BK);
   };
 
   v4i acc[8][4];
@@ -615,13 +645,15 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
   const uint32_t rd = (uint32_t)((lane & 15) * BK + (((lane >> 4) ^ lds_swz(lane & 15)) << 4));
   const uint32_t rda = rd + (uint32_t)(wm * 128 * BK), rdb = rd + (uint32_t)(A_ST + wn * 64 * BK);
   const int nk = (int)(Kpad / BK);
-  issue(0, 0);
-  issue(ST, nk > 1 ? BK : 0);  // two groups always in flight before the loop
-  uint32_t st_rd = 0, st_is = 2 * ST;
+  // STAGES - 1 groups in flight before the loop (clamped to the last step,
+  // so short K still issues the same number of groups).
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; s++) issue((uint32_t)(s * ST), (uint32_t)(s < nk ? s : nk - 1) * BK);
+  uint32_t st_rd = 0, st_is = (uint32_t)((STAGES - 1) * ST);
   for (int kt = 0; kt < nk; kt++) {
-    // Loads of steps kt+1 (and the step issued last iteration) may stay in
-    // flight; step kt's six DMA instructions must have landed.
-    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    // Loads of the STAGES - 2 later steps may stay in flight; step kt's
+    // DMA instructions must have landed.
+    wait_vmcnt<(STAGES - 2) * (IA + IB)>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const int8_t* sa = smem + st_rd;
@@ -632,21 +664,21 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
     for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const v4i*>(sa + rdb + j * 16 * BK);
 #pragma unroll
     for (int i = 0; i < 8; i++) af[i] = *reinterpret_cast<const v4i*>(sa + rda + i * 16 * BK);
-    // Always issue (the last two steps re-fetch step nk-1 into the stage
-    // that is free), so both control paths keep the same counter state and
-    // the MFMAs below wait for their own fragments only.
-    issue(st_is, (uint32_t)(kt + 2 < nk ? kt + 2 : nk - 1) * BK);
+    // Always issue (the last steps re-fetch step nk-1 into the stage that is
+    // free), so every path keeps the same counter state and the MFMAs below
+    // wait for their own fragments only.
+    issue(st_is, (uint32_t)(kt + STAGES - 1 < nk ? kt + STAGES - 1 : nk - 1) * BK);
 #pragma unroll
     for (int i = 0; i < 8; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    st_rd = st_rd == 2 * ST ? 0 : st_rd + ST;
-    st_is = st_is == 2 * ST ? 0 : st_is + ST;
+    st_rd = st_rd == (uint32_t)((STAGES - 1) * ST) ? 0 : st_rd + ST;
+    st_is = st_is == (uint32_t)((STAGES - 1) * ST) ? 0 : st_is + ST;
   }
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(absmax_in_bits)) * ep.w_scale;
+  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
   uint32_t amax = 0;
 #define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
   switch (ep.act) {
@@ -665,12 +697,24 @@ __global__ __launch_bounds__(256, 2) void gemm_i8_big_kernel(const int8_t* __res
   }
 }
 
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
+static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                       int64_t Kpad, const Epilogue& ep, hipStream_t s) {
+  const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
+  hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>), dim3((unsigned)(tm * tn)),
+                     dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep);
+}
+
+// Kernel choice by how many tiles of each shape fill the 256 CUs.
 void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
-  const int64_t big_tiles = (Mpad / big::BM) * (Npad / big::BN);
-  if (big_tiles >= 256 && Mpad % big::BM == 0 && Npad % big::BN == 0 && Kpad % big::BK == 0) {
-    hipLaunchKernelGGL(gemm_i8_big_kernel, dim3((unsigned)big_tiles), dim3(256), 0, s, A, B, M, N, Kpad,
-                       (int)(Mpad / big::BM), (int)(Npad / big::BN), ep);
+  const bool kok = Kpad % big::BK == 0;
+  if (kok && Mpad % 256 == 0 && Npad % 256 == 0 && (Mpad / 256) * (Npad / 256) >= 256) {
+    launch_big<256, 256, 2, 4, 4, 1>(A, B, M, N, Mpad, Npad, Kpad, ep, s);
+    return;
+  }
+  if (kok && Mpad % 256 == 0 && Npad % 128 == 0 && (Mpad / 256) * (Npad / 128) >= 256) {
+    launch_big<256, 128, 2, 2, 3, 2>(A, B, M, N, Mpad, Npad, Kpad, ep, s);
     return;
   }
   constexpr int TM = 128, TN = 128;
