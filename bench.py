@@ -202,6 +202,16 @@ def main():
         "wall_s_timed_region": round(wall, 4),
         "roofline": roof,
     }
+    # PCIe-inclusive rate: InferenceSession.run with host buffers (H2D of the
+    # input, the run, D2H of the output), wall clock; reported beside value.
+    n_host = max(2, min(args.steps, 5))
+    sess.run(x)
+    h0 = time.perf_counter()
+    for _ in range(n_host):
+        sess.run(x)
+    host_s = (time.perf_counter() - h0) / n_host
+    line["pcie_inclusive"] = {"value": round(batch / host_s, 2), "unit": "samples/s", "ms_per_step": round(host_s * 1e3, 3),
+                              "steps": n_host, "note": "host-pointer run(): H2D input + run + D2H output, wall clock"}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds)
     print(json.dumps(line), flush=True)
