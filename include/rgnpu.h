@@ -120,10 +120,12 @@ int rgnpu_program_synchronize(rgnpu_program* prog);
 
 /* Throughput measurement on device buffers: enqueues `iters` runs back to
  * back on the program's stream, bracketed by two HIP events, waits, and
- * returns the elapsed device time.  With per_kernel_events, every run also
- * records per-op events and avg[i] receives op i's mean op time (ns) and
- * main-kernel time (kernel_ns) over the iterations.  No counterpart in the
- * reference; this is the bench harness's timed region. */
+ * returns the elapsed device time.  With per_kernel_events, every kernel of
+ * every run records the completion timestamp of its own dispatch (no marker
+ * packets, so the region is not perturbed) and avg[i] receives op i's mean
+ * op time (ns, from the previous kernel's completion to its last kernel's)
+ * and main-kernel time (kernel_ns) over the iterations.  No counterpart in
+ * the reference; this is the bench harness's timed region. */
 int rgnpu_program_benchmark(rgnpu_program* prog, const float* d_x, const int64_t* shape, int32_t ndim, float* d_y,
                             int64_t y_cap, int32_t iters, int32_t per_kernel_events, double* total_ms,
                             rgnpu_op_record* avg, int32_t cap);

@@ -8,6 +8,7 @@
 // Conv2d (npu.rs:319-383) runs as an implicit GEMM whose im2col gather is
 // done while filling the LDS tile; MaxPool2d (kernels.rs:165-213) is a
 // bandwidth kernel that can emit per-image absmax for the following conv.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <stdexcept>
@@ -18,6 +19,29 @@
 namespace rgnpu {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Launch-event sink (see set_launch_events): every kernel launched while it
+// is set carries the next event as the stop event of its own dispatch.
+static thread_local hipEvent_t* t_sink = nullptr;
+static thread_local int t_sink_cap = 0, t_sink_used = 0;
+
+void set_launch_events(hipEvent_t* events, int cap) {
+  t_sink = events;
+  t_sink_cap = cap;
+  t_sink_used = 0;
+}
+
+int launch_events_used() { return t_sink_used; }
+
+#define RG_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                   \
+  do {                                                                                                     \
+    if (t_sink && t_sink_used < t_sink_cap) {                                                              \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, nullptr, t_sink[t_sink_used++], 0,         \
+                            __VA_ARGS__);                                                                  \
+    } else {                                                                                               \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                                 \
+    }                                                                                                      \
+  } while (0)
 
 // ---------------------------------------------------------------------------
 // small helpers
@@ -89,7 +113,7 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
 void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {
   if (n <= 0) return;
   int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+  RG_LAUNCH(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -178,10 +202,10 @@ void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slo
   if (bx > cap) bx = cap;
   if (bx < 1) bx = 1;
   if (rowmask)
-    hipLaunchKernelGGL(absmax_masked_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
+    RG_LAUNCH(absmax_masked_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
                        rowmask, colmask, (int)H, (int)W);
   else
-    hipLaunchKernelGGL(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
+    RG_LAUNCH(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
                        spread ? 1 : 0);
 }
 
@@ -243,10 +267,10 @@ void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64
   if (blocks > 8192) blocks = 8192;
   const bool vec = (K % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL(quant_rows_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
+    RG_LAUNCH(quant_rows_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
                        scale_out);
   else
-    hipLaunchKernelGGL(quant_rows_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
+    RG_LAUNCH(quant_rows_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad, slot, q,
                        scale_out);
 }
 
@@ -273,7 +297,7 @@ void launch_quant_images(const float* x, int64_t per_img, int64_t n_img, const u
   if (per_img <= 0 || n_img <= 0) return;
   int64_t bx = (per_img + 255) / 256;
   if (bx > 1024) bx = 1024;
-  hipLaunchKernelGGL(quant_images_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots, q,
+  RG_LAUNCH(quant_images_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots, q,
                      scales_out);
 }
 
@@ -701,7 +725,7 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
 static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                        int64_t Kpad, const Epilogue& ep, hipStream_t s) {
   const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
-  hipLaunchKernelGGL((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>), dim3((unsigned)(tm * tn)),
+  RG_LAUNCH((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>), dim3((unsigned)(tm * tn)),
                      dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep);
 }
 
@@ -719,7 +743,7 @@ void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
   }
   constexpr int TM = 128, TN = 128;
   dim3 grid((unsigned)(Npad / TN), (unsigned)(Mpad / TM));
-  hipLaunchKernelGGL((gemm_i8_kernel<TM, TN>), grid, dim3(256), 0, s, A, B, M, N, Kpad, ep);
+  RG_LAUNCH((gemm_i8_kernel<TM, TN>), grid, dim3(256), 0, s, A, B, M, N, Kpad, ep);
 }
 
 // ---------------------------------------------------------------------------
@@ -904,7 +928,7 @@ void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, in
   int64_t blocks = (groups + 3) / 4;
   const int64_t lim = max_blocks > 0 ? max_blocks : cap;
   if (blocks > lim) blocks = lim;
-  hipLaunchKernelGGL((gemv_i8_kernel<MR, R, U>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
+  RG_LAUNCH((gemv_i8_kernel<MR, R, U>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
 }
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
@@ -1021,10 +1045,10 @@ void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const 
   const unsigned gx = (unsigned)((L + TN - 1) / TN);
   if (cs.Opad % 64 == 0) {
     dim3 grid(gx, (unsigned)(cs.Opad / 64), (unsigned)cs.n);
-    hipLaunchKernelGGL((conv_i8_kernel<64, TN>), grid, dim3(256), 0, s, xq, Wq, cs, ep);
+    RG_LAUNCH((conv_i8_kernel<64, TN>), grid, dim3(256), 0, s, xq, Wq, cs, ep);
   } else {
     dim3 grid(gx, (unsigned)(cs.Opad / 32), (unsigned)cs.n);
-    hipLaunchKernelGGL((conv_i8_kernel<32, TN>), grid, dim3(256), 0, s, xq, Wq, cs, ep);
+    RG_LAUNCH((conv_i8_kernel<32, TN>), grid, dim3(256), 0, s, xq, Wq, cs, ep);
   }
 }
 
@@ -1032,32 +1056,52 @@ void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const 
 // Max pool: window scan in (ki, kj) order from -inf with `v > best || NaN`
 // (kernels.rs:180-191), so NaN propagates and ties keep the first element.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void maxpool_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t C,
-                                                      int64_t H, int64_t W, int64_t k, int64_t st, int64_t OH,
-                                                      int64_t OW, uint32_t* absmax_out, int per_image) {
+// Grid: y = image, x = contiguous chunks of that image's C*OH*OW outputs
+// (32-bit index math within an image).  The next op's absmax is reduced per
+// block and raised with one atomic: per image when a conv consumes it, else
+// into the block's partial of a spread slot.  Per-wave atomics on one image
+// slot were the pool's bottleneck (memory-side atomics serialise).
+__global__ __launch_bounds__(256) void maxpool_kernel(const float* __restrict__ x, float* __restrict__ y, uint32_t C,
+                                                      uint32_t H, uint32_t W, uint32_t k, uint32_t st, uint32_t OH,
+                                                      uint32_t OW, uint32_t chunk, uint32_t* absmax_out,
+                                                      int per_image) {
   const int64_t b = blockIdx.y;
-  const int64_t per = C * OH * OW;
+  const uint32_t hw = OH * OW, per = C * hw;
+  const float* xi = x + b * (int64_t)C * H * W;
+  float* yi = y + b * (int64_t)per;
+  const uint32_t e0 = blockIdx.x * chunk;
+  const uint32_t e1 = per - e0 < chunk ? per : e0 + chunk;
   uint32_t amax = 0;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < per; e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t c = e / (OH * OW), rem = e % (OH * OW);
-    const int64_t oy = rem / OW, ox = rem % OW;
-    const float* plane = x + (b * C + c) * H * W;
+  for (uint32_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
+    const uint32_t c = e / hw, r = e - c * hw;
+    const uint32_t oy = r / OW, ox = r - oy * OW;
+    const float* pl = xi + (size_t)c * H * W + (size_t)(oy * st) * W + ox * st;
     float best = -__builtin_inff();
-    for (int64_t ki = 0; ki < k; ki++)
-      for (int64_t kj = 0; kj < k; kj++) {
-        const float v = plane[(oy * st + ki) * W + ox * st + kj];
+    for (uint32_t ki = 0; ki < k; ki++)
+      for (uint32_t kj = 0; kj < k; kj++) {
+        const float v = pl[ki * W + kj];
         if (v > best || v != v) best = v;
       }
-    y[b * per + e] = best;
+    yi[e] = best;
     const uint32_t kk = rgmath::absmax_key(best);
     amax = kk > amax ? kk : amax;
   }
   if (absmax_out) {
     amax = wave_max_u32(amax);
-    if (per_image) {
-      if ((threadIdx.x & 63) == 0 && amax) atomicMax(absmax_out + b, amax);
-    } else if ((threadIdx.x & 63) == 0) {
-      spread_max(absmax_out, amax);
+    __shared__ uint32_t red[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t m = lane < (int)(blockDim.x >> 6) ? red[lane] : 0u;
+      m = wave_max_u32(m);
+      if (lane == 0) {
+        if (per_image) {
+          if (m) atomicMax(absmax_out + b, m);
+        } else {
+          spread_max(absmax_out, m);
+        }
+      }
     }
   }
 }
@@ -1066,10 +1110,16 @@ void launch_maxpool(const float* x, float* y, int64_t n, int64_t C, int64_t H, i
                     int64_t OH, int64_t OW, uint32_t* absmax_out, int absmax_per_image, hipStream_t s) {
   const int64_t per = C * OH * OW;
   if (per <= 0 || n <= 0) return;
-  int64_t bx = (per + 255) / 256;
-  if (bx > 1024) bx = 1024;
-  hipLaunchKernelGGL(maxpool_kernel, dim3((unsigned)bx, (unsigned)n), dim3(256), 0, s, x, y, C, H, W, k, stride, OH,
-                     OW, absmax_out, absmax_per_image);
+  if (C * H * W >= ((int64_t)1 << 32) || n > 65535)
+    throw std::logic_error("max pool: image or batch too large for the 32-bit kernel indexing");
+  // about 16 outputs per thread, at most 64 blocks per image
+  int64_t bx = (per + 256 * 16 - 1) / (256 * 16);
+  if (bx > 64) bx = 64;
+  const int64_t chunk = (per + bx - 1) / bx;
+  bx = (per + chunk - 1) / chunk;
+  RG_LAUNCH(maxpool_kernel, dim3((unsigned)bx, (unsigned)n), dim3(256), 0, s, x, y, (uint32_t)C, (uint32_t)H,
+               (uint32_t)W, (uint32_t)k, (uint32_t)stride, (uint32_t)OH, (uint32_t)OW, (uint32_t)chunk, absmax_out,
+               absmax_per_image);
 }
 
 // ---------------------------------------------------------------------------
@@ -1110,7 +1160,7 @@ void launch_activation(const float* x, float* y, int64_t n, int act, float p, ui
   if (n <= 0) return;
   int64_t blocks = (n + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(activation_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, act, p, absmax_out);
+  RG_LAUNCH(activation_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, y, n, act, p, absmax_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -1137,7 +1187,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float* __restrict__ 
 
 void launch_softmax(const float* x, float* y, int64_t outer, int64_t size, hipStream_t s) {
   if (outer <= 0 || size <= 0) return;
-  hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)((outer + 255) / 256)), dim3(256), 0, s, x, y, outer, size);
+  RG_LAUNCH(softmax_kernel, dim3((unsigned)((outer + 255) / 256)), dim3(256), 0, s, x, y, outer, size);
 }
 
 }  // namespace rgnpu

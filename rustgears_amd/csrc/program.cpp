@@ -17,6 +17,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <array>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -131,6 +132,10 @@ struct Plan {
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
   std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
   bool capture_ready = false;
+  // Per op, indices into the run's launch events (-1 = the run-start event):
+  // [0] last launch before the op, [1] last launch before its main kernel,
+  // [2] its main kernel (== [1] when the op launches none).
+  std::vector<std::array<int, 3>> roles;
 };
 
 }  // namespace rgnpu
@@ -147,7 +152,7 @@ struct rgnpu_program {
   int profiling = 1;
   bool capture = false;
   bool capture_valid = false;
-  std::vector<hipEvent_t> ev;  // run start/end + 4 per op
+  std::vector<hipEvent_t> ev;  // run start/end + launch events
   bool profile_pending = false;
   bool have_profile = false;
   rgnpu_profile prof{};
@@ -560,23 +565,55 @@ static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
   return *P->plan;
 }
 
+// Events of one run: [0], [1] bracket the run (markers, default flags; the
+// host waits on [1]); [2 ..] are launch events: the stop event of each kernel
+// the run launches, recorded by that kernel's own dispatch.  Launch events
+// skip the system-scope fence, which is not needed for timing.  A run
+// launches at most one fill plus three kernels per op.
+static size_t launch_event_cap(const rgnpu_program* P) { return 1 + 3 * P->ops.size(); }
+static size_t events_per_run(const rgnpu_program* P) { return 2 + launch_event_cap(P); }
+
+static void create_run_event(hipEvent_t* e, size_t index_in_set) {
+  if (index_in_set < 2)
+    RG_HIP(hipEventCreate(e));
+  else
+    RG_HIP(hipEventCreateWithFlags(e, hipEventDisableSystemFence));
+}
+
 static void ensure_events(rgnpu_program* P) {
-  const size_t need = 2 + 4 * P->ops.size();
+  const size_t need = events_per_run(P);
   while (P->ev.size() < need) {
     hipEvent_t e;
-    RG_HIP(hipEventCreate(&e));
+    create_run_event(&e, P->ev.size());
     P->ev.push_back(e);
   }
 }
 
-// Enqueue one run; x and y are device pointers.  `ev` holds 2 + 4*ops
-// events (run start/end, then per op: op start, kernel start, kernel end,
-// op end); per-op events are recorded only when `per_op` is set.
-static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, const hipEvent_t* ev, bool per_op) {
+// Per-op (op ns, kernel ns) of one run from its event set.
+static void op_times(const rgnpu_program* P, const Plan& plan, const hipEvent_t* set, size_t i, double* op_ms,
+                     double* kernel_ms) {
+  auto at = [&](int idx) { return idx < 0 ? set[0] : set[2 + idx]; };
+  const auto& r = plan.roles[i];
+  float a = 0, b = 0;
+  if (r[2] != r[0]) RG_HIP(hipEventElapsedTime(&a, at(r[0]), at(r[2])));
+  if (r[2] != r[1]) RG_HIP(hipEventElapsedTime(&b, at(r[1]), at(r[2])));
+  *op_ms = a;
+  *kernel_ms = b;
+  (void)P;
+}
+
+// Enqueue one run; x and y are device pointers.  `ev` is one run's event set
+// (events_per_run): [0] and [1] are always recorded; with `timed` every kernel
+// also records its launch event and plan.roles says which ones bound each op.
+static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipEvent_t* ev, bool timed) {
   hipStream_t s = P->stream;
-  const bool prof = per_op;
   const bool cap = P->capture;
+  struct SinkOff {
+    ~SinkOff() { set_launch_events(nullptr, 0); }
+  } sink_off;
+  set_launch_events(timed ? ev + 2 : nullptr, timed ? (int)launch_event_cap(P) : 0);
   if (cap) ensure_capture_buffers(P, plan);
+  plan.roles.assign(P->ops.size(), std::array<int, 3>{-1, -1, -1});
   RG_HIP(hipEventRecord(ev[0], s));
   uint32_t* slots = plan.slots.as<uint32_t>();
   float* scales = plan.scales.as<float>();
@@ -590,8 +627,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
   for (size_t i = 0; i < P->ops.size(); i++) {
     const Op& op = *P->ops[i];
     const OpPlan& pl = plan.ops[i];
-    hipEvent_t ev_op0 = ev[2 + 4 * i], ev_k0 = ev[3 + 4 * i], ev_k1 = ev[4 + 4 * i], ev_op1 = ev[5 + 4 * i];
-    if (prof) RG_HIP(hipEventRecord(ev_op0, s));
+    const int first = launch_events_used();
+    int pre = first;  // launches before the op's main kernel
     const float* in = buf(pl.in_buf);
     float* out = buf(pl.out_buf);
     uint32_t* emit = pl.emit_slot >= 0 ? slots + pl.emit_slot : nullptr;
@@ -610,14 +647,13 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
         ep.absmax_out = emit;
         ep.absmax_out_per_image = 0;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
-        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        pre = launch_events_used();
         if (pl.rows > 0) {
           if (pl.gemv)
             launch_gemv(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
           else
             launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, s);
         }
-        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
         break;
       }
@@ -643,36 +679,29 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
         ep.absmax_out = emit;
         ep.absmax_out_per_image = pl.emit_per_image;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
-        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        pre = launch_events_used();
         if (c.n > 0 && c.OH * c.OW > 0) launch_conv(q, op.d_w.as<int8_t>(), c, ep, s);
-        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)pl.in_len, hipMemcpyDeviceToDevice, s));
         break;
       }
       case OP_POOL: {
         const auto& is = pl.in_shape;
-        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        pre = launch_events_used();
         launch_maxpool(in, out, is[0], is[1], is[2], is[3], op.k, op.s, pl.out_shape[2], pl.out_shape[3], emit,
                        pl.emit_per_image, s);
-        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
         break;
       }
       case OP_FLATTEN:
-        if (prof) {
-          RG_HIP(hipEventRecord(ev_k0, s));
-          RG_HIP(hipEventRecord(ev_k1, s));
-        }
+        pre = launch_events_used();
         break;
       case OP_ACT:
-        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        pre = launch_events_used();
         launch_activation(in, out, pl.in_len, op.act, op.act_param, emit, s);
-        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
         break;
       case OP_SOFTMAX: {
         const int64_t last = pl.in_shape.back();
-        if (prof) RG_HIP(hipEventRecord(ev_k0, s));
+        pre = launch_events_used();
         if (last > 0) launch_softmax(in, out, pl.in_len / last, last, s);
-        if (prof) RG_HIP(hipEventRecord(ev_k1, s));
         break;
       }
     }
@@ -680,7 +709,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, cons
     if (cap)
       RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),
                             hipMemcpyDeviceToDevice, s));
-    if (prof) RG_HIP(hipEventRecord(ev_op1, s));
+    const int end = launch_events_used();
+    plan.roles[i] = {first - 1, pre - 1, end > pre ? end - 1 : pre - 1};
   }
   // A program with no computing op returns its input (Flatten only).
   bool any = false;
@@ -718,11 +748,10 @@ static void finalize_profile(rgnpu_program* P) {
     r.macs = plan.ops[i].macs;
     total_macs += r.macs;
     if (P->profiling > 0) {
-      float a = 0, b = 0;
-      RG_HIP(hipEventElapsedTime(&a, P->ev[2 + 4 * i], P->ev[5 + 4 * i]));
-      RG_HIP(hipEventElapsedTime(&b, P->ev[3 + 4 * i], P->ev[4 + 4 * i]));
-      r.ns = (uint64_t)((double)a * 1e6);
-      r.kernel_ns = (uint64_t)((double)b * 1e6);
+      double a = 0, b = 0;
+      op_times(P, plan, P->ev.data(), i, &a, &b);
+      r.ns = (uint64_t)(a * 1e6);
+      r.kernel_ns = (uint64_t)(b * 1e6);
     }
   }
   pr.total_macs = total_macs;
@@ -847,7 +876,7 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
   RG_HIP(hipSetDevice(P->device));
   Plan& plan = get_plan(P, shape, ndim);
   if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
-  const size_t per = 2 + 4 * P->ops.size();
+  const size_t per = events_per_run(P);
   const size_t sets = per_kernel_events ? (size_t)iters : 1;
   std::vector<hipEvent_t> evs(per * sets + 2, nullptr);
   struct Guard {
@@ -857,12 +886,17 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
         if (e) (void)hipEventDestroy(e);
     }
   } guard{evs};
-  for (auto& e : evs) RG_HIP(hipEventCreate(&e));
+  for (size_t i = 0; i < evs.size(); i++) {
+    if (i >= (size_t)(per * sets))
+      RG_HIP(hipEventCreate(&evs[i]));  // the region's own start/end
+    else
+      create_run_event(&evs[i], i % (size_t)per);
+  }
   hipEvent_t t0 = evs[per * sets], t1 = evs[per * sets + 1];
   RG_HIP(hipStreamSynchronize(P->stream));
   RG_HIP(hipEventRecord(t0, P->stream));
   for (int32_t it = 0; it < iters; it++) {
-    const hipEvent_t* set = evs.data() + (per_kernel_events ? per * (size_t)it : 0);
+    hipEvent_t* set = evs.data() + (per_kernel_events ? per * (size_t)it : 0);
     enqueue(P, plan, d_x, d_y, set, per_kernel_events != 0);
   }
   RG_HIP(hipEventRecord(t1, P->stream));
@@ -878,10 +912,8 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
       if (per_kernel_events) {
         double a = 0, b = 0;
         for (int32_t it = 0; it < iters; it++) {
-          const hipEvent_t* set = evs.data() + per * (size_t)it;
-          float x = 0, y = 0;
-          RG_HIP(hipEventElapsedTime(&x, set[2 + 4 * i], set[5 + 4 * i]));
-          RG_HIP(hipEventElapsedTime(&y, set[3 + 4 * i], set[4 + 4 * i]));
+          double x = 0, y = 0;
+          op_times(P, plan, evs.data() + per * (size_t)it, i, &x, &y);
           a += x;
           b += y;
         }

@@ -40,6 +40,15 @@ struct Epilogue {
 };
 
 // ---- launchers (kernels.hip) -------------------------------------------
+// Launch events: while set_launch_events(events, cap) is active on this
+// thread, the i-th kernel launched by the launchers below records events[i]
+// as the stop event of its own dispatch (hipExtLaunchKernelGGL), i.e. the
+// completion timestamp of that kernel, with no marker packet and no bubble
+// before the next kernel.  launch_events_used() counts the launches so far.
+// set_launch_events(nullptr, 0) turns it off.
+void set_launch_events(hipEvent_t* events, int cap);
+int launch_events_used();
+
 void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 
 // Absmax of x (f32) (atomic max of |x| bits, NaN ignored): per image into
