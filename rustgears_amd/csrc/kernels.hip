@@ -521,6 +521,34 @@ constexpr int SLAB = 16 * SLAB_LD * 4;
 constexpr int GROUP_M = 8;
 }  // namespace big
 
+// Workgroups of 256 threads of `fn` that are resident on the device at once.
+static int64_t resident_blocks(const void* fn) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
+  return (int64_t)per_cu * cus;
+}
+
+// XCD-aware, M-grouped tile order: hardware deals workgroups round-robin
+// over the 8 XCDs, so tile index t runs on XCD t & 7; the tiles of one XCD
+// are numbered contiguously (L) and walk groups of GROUP_M M-tiles, which
+// keeps their A and B panels in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int xcd = t & 7, local = t >> 3;
+  const int q = total >> 3, rem = total & 7;
+  const int L = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + local;
+  const int group_span = big::GROUP_M * tiles_n;
+  const int group = L / group_span;
+  const int first_m = group * big::GROUP_M;
+  const int gsize = min(tiles_m - first_m, big::GROUP_M);
+  const int in_group = L - group * group_span;
+  tm = first_m + in_group % gsize;
+  tn = in_group / gsize;
+}
+
 // One global_load_lds_dwordx4: 16 bytes per lane, lane i lands at lds + 16 i
 // (the LDS address is wave-uniform).  Kept out of the kernel templates: the
 // LDS address-space cast does not survive the host compilation pass of a
@@ -613,19 +641,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-  // XCD-aware, M-grouped tile order.
-  const int total = tiles_m * tiles_n;
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7, local = bid >> 3;
-  const int q = total >> 3, rem = total & 7;
-  const int L = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + local;
-  const int group_span = GROUP_M * tiles_n;
-  const int group = L / group_span;
-  const int first_m = group * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
-  const int in_group = L - group * group_span;
-  const int tile_m = first_m + in_group % gsize;
-  const int tile_n = in_group / gsize;
+  int tile_m, tile_n;
+  tile_coords(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
   const int64_t m0 = (int64_t)tile_m * BM, n0 = (int64_t)tile_n * BN;
   // Epilogue operands are fetched now; they arrive while the K loop runs.
   const int64_t my_col = n0 + wn * 64 + lane;
@@ -909,15 +926,6 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__
   }
 }
 
-// Workgroups of 256 threads of `fn` that are resident on the device at once.
-static int64_t resident_blocks(const void* fn) {
-  int dev = 0, cus = 0, per_cu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) per_cu = 1;
-  return (int64_t)per_cu * cus;
-}
 
 template <int MR, int R, int U>
 void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, int64_t Kpad, const Epilogue& ep,
