@@ -32,17 +32,6 @@
 #define RG_HD static inline
 #endif
 
-// Keeps a value computed unconditionally on the GPU.  The branch-free forms
-// below compute every case and select; without this the compiler sinks each
-// case into an exec-masked branch, which costs scalar branching, splits the
-// basic block (no interleaving with MFMA work) and still runs every case
-// under divergence.  Changes no value.
-#if defined(__HIP_DEVICE_COMPILE__)
-#define RG_KEEP(x) asm("" : "+v"(x))
-#else
-#define RG_KEEP(x) ((void)0)
-#endif
-
 namespace rgmath {
 
 RG_HD uint32_t fbits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -221,7 +210,7 @@ RG_HD float expm1f_tanh_domain(float x) {
   const float e = hxs * div_fast(num, den);
   // k == 0
   const float xe = xr * e;
-  float r0 = xr - (xe - hxs);
+  const float r0 = xr - (xe - hxs);
   // k != 0 share e2 = x*(e-c) - c - hxs
   const float ec = e - c;
   float e2 = xr * ec;
@@ -230,23 +219,18 @@ RG_HD float expm1f_tanh_domain(float x) {
   const float em = e2 - xr;
   // k == -1
   const float d1 = xr - e2;
-  float rm1 = 0.5f * d1 - 0.5f;
+  const float rm1 = 0.5f * d1 - 0.5f;
   // k <= -2 or k > 56
   const uint32_t kshift = (uint32_t)k << 23;
   const float ylow = 1.0f - em;
-  float rlow = bitsf(fbits(ylow) + kshift) - 1.0f;
+  const float rlow = bitsf(fbits(ylow) + kshift) - 1.0f;
   // 2 <= k < 23: t = 1 - 2^-k
   const float tk = bitsf(0x3f800000u - (0x1000000u >> (k & 31)));
-  float rmid = bitsf(fbits(tk - em) + kshift);
+  const float rmid = bitsf(fbits(tk - em) + kshift);
   // 23 <= k <= 56: t = 2^-k
   const float t2 = bitsf(((uint32_t)(0x7f - k) & 0x1ffu) << 23);
   const float yh = (xr - (e2 + t2)) + 1.0f;
-  float rhigh = bitsf(fbits(yh) + kshift);
-  RG_KEEP(r0);
-  RG_KEEP(rm1);
-  RG_KEEP(rlow);
-  RG_KEEP(rmid);
-  RG_KEEP(rhigh);
+  const float rhigh = bitsf(fbits(yh) + kshift);
   float r = k == 0 ? r0 : (k == -1 ? rm1 : ((k <= -2 || k > 56) ? rlow : (k < 23 ? rmid : rhigh)));
   return hx < 0x33000000u ? x : r;
 }
@@ -263,10 +247,8 @@ RG_HD float tanhf_fast(float x) {
   const float q = div_fast(ge1 ? 2.0f : -t, d);
   float z = ge1 ? 1.0f - q : q;
   z = ix >= 0x41b00000u ? 1.0f : z;                // |x| >= 22 (and +-inf)
-  float signed_z = (jx >> 31) ? -z : z;
-  float tiny = x * (1.0f + x);                     // |x| < 2^-55, and +-0
-  RG_KEEP(signed_z);
-  RG_KEEP(tiny);
+  const float signed_z = (jx >> 31) ? -z : z;
+  const float tiny = x * (1.0f + x);               // |x| < 2^-55, and +-0
   float r = ix < 0x24000000u ? tiny : signed_z;
   return ix > 0x7f800000u ? x + x : r;             // NaN
 }
