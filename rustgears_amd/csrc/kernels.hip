@@ -954,12 +954,183 @@ void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// Implicit-GEMM conv.  MFMA "A" = weights [Opad, Kpad] (TM output channels),
-// "B" = im2col columns of one image (TN output pixels), so D[o][l] maps onto
-// the NCHW output with pixels contiguous.  The B tile is gathered from the
-// quantized image while it is written to LDS; out-of-image taps and K padding
-// are zeros.  Each of the 4 waves owns all TM channels x TN/4 pixels.
+// Implicit-GEMM conv.  MFMA "A" = weights [Opad, Kpad] (TM output channels,
+// tap-major K, see ConvShape), "B" = im2col columns of one image (output
+// pixels), so D[o][l] maps onto the NCHW output with pixels contiguous.
+//
+// Main kernel (conv_band_kernel): block = image b (grid.z) x TM channels
+// (grid.y) x TN pixels (grid.x); wave w owns pixels [p0 + w TN/4, +TN/4).
+// LDS holds the block's weights (row stride Kpad + 16) and the input rows its
+// pixels read, zero padded and channel-last: band[r][x][c], r < R,
+// x < W + 2 pad, c < cp.  A 16-byte K chunk of an im2col column is then 16
+// channels of one tap (cp >= 16: one ds_read_b128) or 4 channels of 4 taps
+// (cp == 4: four ds_read_b32); taps past k*k read a zero block.  Outputs are
+// stored straight from the accumulators (16 consecutive pixels per store).
 // ---------------------------------------------------------------------------
+struct ConvBand {
+  int rows_max;    // band rows for the worst block
+  int lds_bytes;   // dynamic LDS
+};
+
+static ConvBand conv_band_geom(const ConvShape& cs, int TM, int TN) {
+  const int64_t Wp = cs.W + 2 * cs.pad;
+  const int64_t rows = ((TN - 1) / cs.OW + 1) * cs.stride + cs.k;
+  const int64_t band = round_up(rows * Wp * cs.cp, 16) + 16;
+  const int64_t bytes = (int64_t)TM * (cs.Kpad + 16) + band;
+  return ConvBand{(int)rows, bytes > (1 << 30) ? (1 << 30) : (int)bytes};
+}
+
+template <int TM, int TN, bool CP4, int ACT>
+__device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
+                                                   const Epilogue& ep, int b, int o0, const int (&pix)[TN / 64],
+                                                   float csc, int lane) {
+  constexpr int FM = TM / 16, FN = TN / 64;
+  const int64_t O = cs.O, L = cs.OH * cs.OW;
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int o = o0 + i * 16 + (lane >> 4) * 4 + r;
+      const float bias = ep.bias[o];  // padded to Opad
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int p = pix[j];
+        if (o < O && p < L) {
+          const int32_t a = acc[i][j][r];
+          const float v = epi_value<ACT>(a, csc, bias, ep.act_param);
+          ep.y[((int64_t)b * O + o) * L + p] = v;
+          if (ep.acc_out) ep.acc_out[((int64_t)b * L + p) * O + o] = a;
+          const uint32_t key = rgmath::absmax_key(v);
+          amax = key > amax ? key : amax;
+        }
+      }
+    }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (ep.absmax_out_per_image) {
+      if (lane == 0 && amax) atomicMax(ep.absmax_out + b, amax);
+    } else if (lane == 0) {
+      spread_max(ep.absmax_out, amax);
+    }
+  }
+}
+
+template <int TM, int TN, bool CP4>
+__global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ Wt,
+                                                        ConvShape cs, Epilogue ep) {
+  extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+  constexpr int WTN = TN / 4, FM = TM / 16, FN = WTN / 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.z, o0 = blockIdx.y * TM, p0 = blockIdx.x * TN;
+  const int C = (int)cs.C, H = (int)cs.H, W = (int)cs.W, k = (int)cs.k, st = (int)cs.stride, pad = (int)cs.pad;
+  const int OW = (int)cs.OW, L = (int)(cs.OH * cs.OW), KP = (int)cs.Kpad, cp = (int)cs.cp, kk = k * k;
+  const int wstride = KP + 16, Wp = W + 2 * pad;
+  int8_t* const wts = dsm;
+  int8_t* const band = dsm + TM * wstride;
+  const int oy0 = p0 / OW, oy1 = (min(p0 + TN, L) - 1) / OW;
+  const int R = (oy1 - oy0) * st + k;
+  const int band_bytes = R * Wp * cp;
+  int8_t* const zero16 = band + ((band_bytes + 15) & ~15);
+
+  // 1. zero the band and the zero block; copy this block's weights.
+  for (int i = tid; i <= (band_bytes + 15) / 16; i += 256) *reinterpret_cast<v4i*>(band + 16 * i) = v4i{0, 0, 0, 0};
+  const int kc = KP / 16;
+  for (int i = tid; i < TM * kc; i += 256) {
+    const int row = i / kc, c16 = i - row * kc;
+    *reinterpret_cast<v4i*>(wts + row * wstride + c16 * 16) =
+        *reinterpret_cast<const v4i*>(Wt + (int64_t)(o0 + row) * KP + c16 * 16);
+  }
+  __syncthreads();
+  // 2. input rows iy = oy0*st - pad + r of every channel, channel-last.
+  const int8_t* img = xq + (int64_t)b * C * H * W;
+  const int iy_base = oy0 * st - pad;
+  if ((W & 3) == 0) {
+    const int wq = W >> 2, per_c = R * wq;
+    for (int e = tid; e < C * per_c; e += 256) {
+      const int c = e / per_c, t = e - c * per_c, r = t / wq, x = (t - r * wq) * 4;
+      const int iy = iy_base + r;
+      if (iy >= 0 && iy < H) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(img + ((int64_t)c * H + iy) * W + x);
+        int8_t* d = band + (r * Wp + x + pad) * cp + c;
+        d[0] = (int8_t)v;
+        d[cp] = (int8_t)(v >> 8);
+        d[2 * cp] = (int8_t)(v >> 16);
+        d[3 * cp] = (int8_t)(v >> 24);
+      }
+    }
+  } else {
+    const int per_c = R * W;
+    for (int e = tid; e < C * per_c; e += 256) {
+      const int c = e / per_c, t = e - c * per_c, r = t / W, x = t - r * W;
+      const int iy = iy_base + r;
+      if (iy >= 0 && iy < H) band[(r * Wp + x + pad) * cp + c] = img[((int64_t)c * H + iy) * W + x];
+    }
+  }
+  __syncthreads();
+
+  // 3. per-lane pixels and the byte offset of their tap (0, 0), channel 0.
+  int pix[FN], rowoff[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    pix[j] = p0 + wave * WTN + j * 16 + (lane & 15);
+    const int oy = pix[j] / OW, ox = pix[j] - oy * OW;
+    rowoff[j] = pix[j] < L ? ((oy - oy0) * st * Wp + ox * st) * cp : -1;
+  }
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+  for (int k0 = 0; k0 < KP; k0 += 64) {
+    const int kb = k0 + (lane >> 4) * 16;  // this lane's 16-byte K chunk
+    v4i af[FM], bf[FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(wts + (i * 16 + (lane & 15)) * wstride + kb);
+    if (!CP4) {
+      const int tap = kb / cp, c0 = kb - tap * cp;
+      const int ki = tap / k, kj = tap - ki * k;
+      const int toff = (ki * Wp + kj) * cp + c0;
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
+        bf[j] = *reinterpret_cast<const v4i*>(a);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int tap = (kb >> 2) + e;
+        const int ki = tap / k, kj = tap - ki * k;
+        const int toff = (ki * Wp + kj) * 4;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
+          bf[j][e] = *reinterpret_cast<const int*>(a);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
+  const float csc = slot_scale(ep.absmax_in + b) * ep.w_scale;
+  switch (ep.act) {
+    case rgmath::ACT_RELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_RELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_SIGMOID: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SIGMOID>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_TANH: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_TANH>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_GELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_GELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_LEAKY_RELU:
+      conv_band_epilogue<TM, TN, CP4, rgmath::ACT_LEAKY_RELU>(acc, cs, ep, b, o0, pix, csc, lane);
+      break;
+    case rgmath::ACT_SILU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SILU>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    default: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_NONE>(acc, cs, ep, b, o0, pix, csc, lane); break;
+  }
+}
+
+// Fallback for shapes whose band or weights do not fit in LDS: the im2col
+// tile is gathered byte by byte from the quantized image (tap-major K).
 template <int TM, int TN>
 __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ Wq,
                                                       ConvShape cs, Epilogue ep) {
@@ -975,7 +1146,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.z;
   const int64_t o0 = (int64_t)blockIdx.y * TM, p0 = (int64_t)blockIdx.x * TN;
-  const int64_t L = cs.OH * cs.OW, KK = cs.C * cs.k * cs.k, kk2 = cs.k * cs.k;
+  const int64_t L = cs.OH * cs.OW;
+  const int C = (int)cs.C, H = (int)cs.H, W = (int)cs.W, k = (int)cs.k, cp = (int)cs.cp, kk = k * k;
   const int8_t* img = xq + b * cs.C * cs.H * cs.W;
 
   v4i acc[FM][FN];
@@ -988,7 +1160,7 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
   constexpr int KB = kTK * TN / 256;
   const int gp = tid % TN, gk = (tid / TN) * KB;
   const int64_t pix = p0 + gp;
-  const int64_t oy = pix / cs.OW, ox = pix % cs.OW;
+  const int oy = (int)(pix / cs.OW), ox = (int)(pix % cs.OW);
   const bool pix_ok = pix < L;
   const int koff = (lane >> 4) * 16;
 
@@ -1005,13 +1177,13 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
       uint32_t word = 0;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const int64_t kk = k0 + gk + w4 * 4 + e;
+        const int kq = (int)k0 + gk + w4 * 4 + e;  // tap-major index
+        const int tap = kq / cp, ch = kq - tap * cp;
         int8_t v = 0;
-        if (pix_ok && kk < KK) {
-          const int64_t ch = kk / kk2, rem = kk % kk2;
-          const int64_t ki = rem / cs.k, kj = rem % cs.k;
-          const int64_t iy = oy * cs.stride + ki - cs.pad, ix = ox * cs.stride + kj - cs.pad;
-          if (iy >= 0 && iy < cs.H && ix >= 0 && ix < cs.W) v = img[(ch * cs.H + iy) * cs.W + ix];
+        if (pix_ok && tap < kk && ch < C) {
+          const int ki = tap / k, kj = tap - ki * k;
+          const int iy = oy * (int)cs.stride + ki - (int)cs.pad, ix = ox * (int)cs.stride + kj - (int)cs.pad;
+          if (iy >= 0 && iy < H && ix >= 0 && ix < W) v = img[((int64_t)ch * H + iy) * W + ix];
         }
         word |= (uint32_t)(uint8_t)v << (8 * e);
       }
@@ -1047,7 +1219,40 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
   epilogue_tile<TM, TN, CLD, true>(Cs, tc, csc, ep);
 }
 
+template <int TM, int TN, bool CP4>
+static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {
+  const ConvBand g = conv_band_geom(cs, TM, TN);
+  constexpr int kMaxLds = 160 * 1024;
+  if (g.lds_bytes > kMaxLds) return false;
+  const void* fn = reinterpret_cast<const void*>(&conv_band_kernel<TM, TN, CP4>);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess) return false;
+    attr_set = true;
+  }
+  const int64_t L = cs.OH * cs.OW;
+  dim3 grid((unsigned)((L + TN - 1) / TN), (unsigned)(cs.Opad / TM), (unsigned)cs.n);
+  RG_LAUNCH((conv_band_kernel<TM, TN, CP4>), grid, dim3(256), (unsigned)g.lds_bytes, s, xq, Wq, cs, ep);
+  return true;
+}
+
+template <int TM, bool CP4>
+static bool try_conv_band_tn(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
+                             hipStream_t s) {
+  return try_conv_band<TM, 256, CP4>(xq, Wq, cs, ep, s) || try_conv_band<TM, 128, CP4>(xq, Wq, cs, ep, s) ||
+         try_conv_band<TM, 64, CP4>(xq, Wq, cs, ep, s);
+}
+
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {
+  if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31))
+    throw std::logic_error("conv: shape too large for the kernel's indexing");
+  const bool cp4 = cs.cp == 4;
+  bool done;
+  if (cs.Opad % 64 == 0)
+    done = cp4 ? try_conv_band_tn<64, true>(xq, Wq, cs, ep, s) : try_conv_band_tn<64, false>(xq, Wq, cs, ep, s);
+  else
+    done = cp4 ? try_conv_band_tn<32, true>(xq, Wq, cs, ep, s) : try_conv_band_tn<32, false>(xq, Wq, cs, ep, s);
+  if (done) return;
   constexpr int TN = 128;
   const int64_t L = cs.OH * cs.OW;
   const unsigned gx = (unsigned)((L + TN - 1) / TN);

@@ -252,9 +252,21 @@ static float quantize_host(const float* v, int64_t n, int8_t* out) {
 }
 
 static void upload_weights(Op& op, hipStream_t s) {
-  // [N, K] host -> [Npad, Kpad] device, zero padded.
+  // Linear: [N, K] host -> [Npad, Kpad] device, zero padded.  Conv: the
+  // reference [O, C*k*k] order becomes tap-major [Opad, Kpad], kk' =
+  // (ki*k + kj)*cp + c (see ConvShape).
   std::vector<int8_t> pad((size_t)(op.Npad * op.Kpad), 0);
-  for (int64_t r = 0; r < op.out_f; r++) std::memcpy(&pad[(size_t)(r * op.Kpad)], &op.wq[(size_t)(r * op.K)], (size_t)op.K);
+  if (op.kind == OP_CONV) {
+    const int64_t C = op.in_f, k = op.k, cp = conv_cp(C);
+    for (int64_t o = 0; o < op.out_f; o++)
+      for (int64_t c = 0; c < C; c++)
+        for (int64_t ki = 0; ki < k; ki++)
+          for (int64_t kj = 0; kj < k; kj++)
+            pad[(size_t)(o * op.Kpad + (ki * k + kj) * cp + c)] = op.wq[(size_t)(o * op.K + (c * k + ki) * k + kj)];
+  } else {
+    for (int64_t r = 0; r < op.out_f; r++)
+      std::memcpy(&pad[(size_t)(r * op.Kpad)], &op.wq[(size_t)(r * op.K)], (size_t)op.K);
+  }
   std::vector<float> bpad((size_t)op.Npad, 0.0f);
   std::memcpy(bpad.data(), op.bias.data(), sizeof(float) * op.bias.size());
   op.d_w.ensure(pad.size());
@@ -335,7 +347,7 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
       P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
       P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
       op->Npad = round_up(op->out_f, kConvOPad);
-      op->Kpad = round_up(op->K, kKPad);
+      op->Kpad = conv_kpad(op->in_f, op->k);
     } else if (f.spec.kind == RGNPU_LAYER_CHANNEL_AFFINE) {
       // Lone ChannelAffine -> diagonal Linear, no byte accounting (npu.rs:254-270).
       const int64_t c = (int64_t)f.scale.size();
@@ -429,7 +441,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         if (c != op.in_f)
           throw Error(RGNPU_ERR_SHAPE, "Conv2d: input has " + std::to_string(c) + " channels, expected " + std::to_string(op.in_f));
         const int64_t oh = out_size(h, op.k, op.s, op.p), ow = out_size(w, op.k, op.s, op.p);
-        pl.cs = ConvShape{n, c, h, w, op.out_f, op.Npad, op.k, op.s, op.p, oh, ow, op.Kpad};
+        pl.cs = ConvShape{n, c, h, w, op.out_f, op.Npad, op.k, op.s, op.p, oh, ow, op.Kpad, conv_cp(c)};
         pl.macs = (uint64_t)(n * op.out_f * op.K * oh * ow);
         auto rm = coverage(h, op.k, op.s, op.p, oh), cm = coverage(w, op.k, op.s, op.p, ow);
         pl.full_cov = true;

@@ -77,10 +77,16 @@ void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
                  int64_t Kpad, const Epilogue& ep, hipStream_t s);
 
 // Implicit-GEMM conv: per image b, y[b,o,l] = act(sum_kk W[o,kk]*im2col(xq_b)[kk,l]
-// * (sa_b*sw) + bias[o]).  xq is i8 NCHW; W is [Opad, Kpad] with kk = (c*k+ki)*k+kj.
+// * (sa_b*sw) + bias[o]).  xq is i8 NCHW.  On the device W is [Opad, Kpad] in
+// tap-major order, kk' = (ki*k + kj)*cp + c with the channels padded to cp
+// (4 when C <= 4, else a multiple of 16) and zero weights for c >= C: the i32
+// sums do not depend on the order of the K terms, and this order makes the
+// im2col operand of one tap a contiguous run of channels.
 struct ConvShape {
-  int64_t n, C, H, W, O, Opad, k, stride, pad, OH, OW, Kpad;
+  int64_t n, C, H, W, O, Opad, k, stride, pad, OH, OW, Kpad, cp;
 };
+inline int64_t conv_cp(int64_t C) { return C <= 4 ? 4 : round_up(C, 16); }
+inline int64_t conv_kpad(int64_t C, int64_t k) { return round_up(k * k * conv_cp(C), 64); }
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
                  hipStream_t s);
 
