@@ -364,129 +364,12 @@ __device__ __forceinline__ void epilogue_tile(const int32_t* Cs, const TileCoord
 }
 
 // ---------------------------------------------------------------------------
-// i8 MFMA GEMM.  Block tile TM x TN, K step 64 bytes, 4 waves in a 2x2 grid,
-// each wave owns (TM/2) x (TN/2) built from 16x16 v_mfma_i32_16x16x64_i8
-// blocks.  Operands are K-contiguous; LDS rows are padded to 80 bytes so the
-// 16 row reads of one MFMA operand fetch hit distinct banks.  Two LDS stages:
-// the next K step is loaded to registers while the current one is consumed.
-//
-// MFMA operand/result layout (16x16x64): lane l supplies row (l%16) of A and
-// column (l%16) of B, K bytes [16*(l/16), 16*(l/16)+16); result register r
-// of lane l holds D[4*(l/16)+r][l%16].
+// MFMA operand/result layout (v_mfma_i32_16x16x64_i8): lane l supplies row
+// (l%16) of A and column (l%16) of B, K bytes [16*(l/16), 16*(l/16)+16);
+// result register r of lane l holds D[4*(l/16)+r][l%16].
 // ---------------------------------------------------------------------------
 constexpr int kTK = 64;
 constexpr int kLdsStride = kTK + 16;
-
-template <int TM, int TN>
-__global__ __launch_bounds__(256) void gemm_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                      int64_t M, int64_t N, int64_t Kpad, Epilogue ep) {
-  constexpr int STAGE = 2 * (TM + TN) * kLdsStride;
-  constexpr int CLD = TN + 4;
-  constexpr int EPI = TM * CLD * 4;
-  __shared__ __attribute__((aligned(16))) int8_t smem[STAGE > EPI ? STAGE : EPI];
-  int8_t* const As = smem;
-  int8_t* const Bs = smem + 2 * TM * kLdsStride;
-  constexpr int WTM = TM / 2, WTN = TN / 2, FM = WTM / 16, FN = WTN / 16;
-  constexpr int A_CH = TM * kTK / 16 / 256, B_CH = TN * kTK / 16 / 256;
-  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small");
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.y * TM, n0 = (int64_t)blockIdx.x * TN;
-
-  v4i acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-
-  // Global -> register -> LDS staging; thread t moves 16-byte chunks
-  // (row = c/4, col = 16*(c%4)) of the TM x 64 and TN x 64 tiles.
-  v4i ra[A_CH], rb[B_CH];
-#pragma unroll
-  for (int i = 0; i < A_CH; i++) {
-    const int c = tid + i * 256;
-    ra[i] = *reinterpret_cast<const v4i*>(A + (m0 + (c >> 2)) * Kpad + (c & 3) * 16);
-  }
-#pragma unroll
-  for (int i = 0; i < B_CH; i++) {
-    const int c = tid + i * 256;
-    rb[i] = *reinterpret_cast<const v4i*>(B + (n0 + (c >> 2)) * Kpad + (c & 3) * 16);
-  }
-#pragma unroll
-  for (int i = 0; i < A_CH; i++) {
-    const int c = tid + i * 256;
-    *reinterpret_cast<v4i*>(&As[(c >> 2) * kLdsStride + (c & 3) * 16]) = ra[i];
-  }
-#pragma unroll
-  for (int i = 0; i < B_CH; i++) {
-    const int c = tid + i * 256;
-    *reinterpret_cast<v4i*>(&Bs[(c >> 2) * kLdsStride + (c & 3) * 16]) = rb[i];
-  }
-  __syncthreads();
-
-  const int64_t nk = Kpad / kTK;
-  const int koff = (lane >> 4) * 16;
-  for (int64_t kt = 0; kt < nk; kt++) {
-    const int cur = (int)(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int64_t k0 = (kt + 1) * kTK;
-#pragma unroll
-      for (int i = 0; i < A_CH; i++) {
-        const int c = tid + i * 256;
-        ra[i] = *reinterpret_cast<const v4i*>(A + (m0 + (c >> 2)) * Kpad + k0 + (c & 3) * 16);
-      }
-#pragma unroll
-      for (int i = 0; i < B_CH; i++) {
-        const int c = tid + i * 256;
-        rb[i] = *reinterpret_cast<const v4i*>(B + (n0 + (c >> 2)) * Kpad + k0 + (c & 3) * 16);
-      }
-    }
-    const int8_t* Ac = As + cur * TM * kLdsStride;
-    const int8_t* Bc = Bs + cur * TN * kLdsStride;
-    v4i af[FM], bf[FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-      af[i] = *reinterpret_cast<const v4i*>(&Ac[(wm * WTM + i * 16 + (lane & 15)) * kLdsStride + koff]);
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-      bf[j] = *reinterpret_cast<const v4i*>(&Bc[(wn * WTN + j * 16 + (lane & 15)) * kLdsStride + koff]);
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    if (more) {
-      int8_t* An = As + (cur ^ 1) * TM * kLdsStride;
-      int8_t* Bn = Bs + (cur ^ 1) * TN * kLdsStride;
-#pragma unroll
-      for (int i = 0; i < A_CH; i++) {
-        const int c = tid + i * 256;
-        *reinterpret_cast<v4i*>(&An[(c >> 2) * kLdsStride + (c & 3) * 16]) = ra[i];
-      }
-#pragma unroll
-      for (int i = 0; i < B_CH; i++) {
-        const int c = tid + i * 256;
-        *reinterpret_cast<v4i*>(&Bn[(c >> 2) * kLdsStride + (c & 3) * 16]) = rb[i];
-      }
-    }
-    __syncthreads();
-  }
-
-  // Stage accumulators in LDS (the stage buffers are free after the barrier).
-  int32_t* Cs = reinterpret_cast<int32_t*>(smem);
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        Cs[(wm * WTM + i * 16 + (lane >> 4) * 4 + r) * CLD + wn * WTN + j * 16 + (lane & 15)] = acc[i][j][r];
-  __syncthreads();
-  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
-  const TileCoords tc{m0, n0, M, N, 0};
-  epilogue_tile<TM, TN, CLD, false>(Cs, tc, cs, ep);
-}
 
 // ---------------------------------------------------------------------------
 // Large-problem i8 GEMM.
@@ -587,12 +470,12 @@ __device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int r
   return amax;
 }
 
-// Stages the wave's 128 x 64 accumulator tile through LDS 16 rows at a time
-// and stores it row-major: lane l owns column n0 + wn*64 + l, so each store
-// instruction writes 256 contiguous bytes.  The bias and scale were loaded
-// before the K loop.
-template <int ACT, bool CAP>
-__device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[8][4], int64_t m0, int64_t n0,
+// Stages the wave's (16 FM) x 64 accumulator tile through LDS 16 rows at a
+// time and stores it row-major: lane l owns column n0 + wn*64 + l, so each
+// store instruction writes 256 contiguous bytes.  The bias and scale were
+// loaded before the K loop.
+template <int ACT, bool CAP, int FM>
+__device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                  int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                  int wave, int wm, int wn, int lane) {
   int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
@@ -602,12 +485,12 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
   // lanes past the last column then store nothing.
   const bool col_ok = col < N;
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < FM; i++) {
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
-    const int64_t row0 = m0 + wm * 128 + i * 16;
+    const int64_t row0 = m0 + wm * (16 * FM) + i * 16;
     const int rows = col_ok ? (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16) : 0;
     float* yp = ep.y + row0 * N + col;
     int32_t* ap = CAP ? ep.acc_out + row0 * N + col : nullptr;
@@ -617,21 +500,23 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
   return amax;
 }
 
-template <int ACT>
-__device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&acc)[8][4], int64_t m0, int64_t n0,
+template <int ACT, int FM>
+__device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                      int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                      int wave, int wm, int wn, int lane) {
-  return ep.acc_out ? big_epilogue<ACT, true>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
-                    : big_epilogue<ACT, false>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
+  return ep.acc_out ? big_epilogue<ACT, true, FM>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
+                    : big_epilogue<ACT, false, FM>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
+// Split K: gridDim.y > 1 gives block (x, y) the K steps [y*ks, (y+1)*ks) and
+// it stores its raw i32 sums to ws[y][Mpad][Npad] for splitk_epilogue_kernel.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int64_t M, int64_t N, int64_t Kpad, int tiles_m,
-    int tiles_n, Epilogue ep) {
+    int tiles_n, Epilogue ep, int ks, int32_t* __restrict__ ws) {
   using namespace big;
   constexpr int NW = WAVES_M * WAVES_N;
-  static_assert(BM == 128 * WAVES_M && BN == 64 * WAVES_N, "wave tile is 128 x 64");
+  static_assert(BM == 16 * FM * WAVES_M && BN == 64 * WAVES_N, "wave tile is (16 FM) x 64");
   constexpr int IA = BM / 16 / NW, IB = BN / 16 / NW;  // DMA instructions per wave per stage
   static_assert(IA * 16 * NW == BM && IB * 16 * NW == BN && IA >= 1 && IB >= 1, "DMA split");
   static_assert(STAGES >= 3, "ring depth");
@@ -668,24 +553,29 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
     const int r = (wave * IB + j) * 16 + lr;
     offb[j] = (uint32_t)r * kp + (uint32_t)((lp ^ lds_swz(r)) << 4);
   }
+  // This block's K steps [kbeg, kbeg + nk); the DMA offsets address K from kbeg.
+  const int nk_all = (int)(Kpad / BK);
+  const int kbeg = (int)blockIdx.y * ks;
+  const int8_t* const abase_k = abase + (int64_t)kbeg * BK;
+  const int8_t* const bbase_k = bbase + (int64_t)kbeg * BK;
   auto issue = [&](uint32_t st_off, uint32_t k0) {
     int8_t* sa = smem + st_off;
 #pragma unroll
-    for (int j = 0; j < IA; j++) dma16(abase + (offa[j] + k0), sa + (wave * IA + j) * 16 * BK);
+    for (int j = 0; j < IA; j++) dma16(abase_k + (offa[j] + k0), sa + (wave * IA + j) * 16 * BK);
 #pragma unroll
-    for (int j = 0; j < IB; j++) dma16(bbase + (offb[j] + k0), sa + A_ST + (wave * IB + j) * 16 * BK);
+    for (int j = 0; j < IB; j++) dma16(bbase_k + (offb[j] + k0), sa + A_ST + (wave * IB + j) * 16 * BK);
   };
 
-  v4i acc[8][4];
+  v4i acc[FM][4];
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
   // MFMA operand read offset: row (lane & 15) of a 16-row block, chunk lane>>4.
   const uint32_t rd = (uint32_t)((lane & 15) * BK + (((lane >> 4) ^ lds_swz(lane & 15)) << 4));
-  const uint32_t rda = rd + (uint32_t)(wm * 128 * BK), rdb = rd + (uint32_t)(A_ST + wn * 64 * BK);
-  const int nk = (int)(Kpad / BK);
+  const uint32_t rda = rd + (uint32_t)(wm * 16 * FM * BK), rdb = rd + (uint32_t)(A_ST + wn * 64 * BK);
+  const int nk = min(ks, nk_all - kbeg);
   // STAGES - 1 groups in flight before the loop (clamped to the last step,
   // so short K still issues the same number of groups).
 #pragma unroll
@@ -700,17 +590,17 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
     const int8_t* sa = smem + st_rd;
     // B fragments first, then A in consumption order, so each MFMA row
     // block waits only for its own A fragment (lgkmcnt counts in order).
-    v4i bf[4], af[8];
+    v4i bf[4], af[FM];
 #pragma unroll
     for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const v4i*>(sa + rdb + j * 16 * BK);
 #pragma unroll
-    for (int i = 0; i < 8; i++) af[i] = *reinterpret_cast<const v4i*>(sa + rda + i * 16 * BK);
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(sa + rda + i * 16 * BK);
     // Always issue (the last steps re-fetch step nk-1 into the stage that is
     // free), so every path keeps the same counter state and the MFMAs below
     // wait for their own fragments only.
     issue(st_is, (uint32_t)(kt + STAGES - 1 < nk ? kt + STAGES - 1 : nk - 1) * BK);
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     st_rd = st_rd == (uint32_t)((STAGES - 1) * ST) ? 0 : st_rd + ST;
@@ -719,9 +609,23 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+  if (gridDim.y > 1) {
+    // Split K: raw sums for splitk_epilogue_kernel (padded extent, no masks).
+    const int64_t Npad = (int64_t)tiles_n * BN;
+    int32_t* w = ws + ((int64_t)blockIdx.y * tiles_m * BM + m0 + wm * 16 * FM + (lane >> 4) * 4) * Npad + n0 +
+                 wn * 64 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) w[(int64_t)(i * 16 + r) * Npad + j * 16] = acc[i][j][r];
+    (void)absmax_part;
+    return;
+  }
   const float cs = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
   uint32_t amax = 0;
-#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
+#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV, FM>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
   switch (ep.act) {
     case rgmath::ACT_RELU: amax = RG_BIG_EPI(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: amax = RG_BIG_EPI(rgmath::ACT_SIGMOID); break;
@@ -738,29 +642,105 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC>
-static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
-                       int64_t Kpad, const Epilogue& ep, hipStream_t s) {
-  const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
-  RG_LAUNCH((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC>), dim3((unsigned)(tm * tn)),
-                     dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep);
+// Split-K epilogue: y = act(float(sum of the S partial sums) * cs + bias).
+template <int ACT>
+__global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ ws, int S, int64_t M,
+                                                              int64_t N, int64_t Mpad, int64_t Npad, Epilogue ep) {
+  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  const int64_t n4 = Npad / 4, total = M * n4;
+  uint32_t amax = 0;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = e / n4, c0 = (e - row * n4) * 4;
+    v4i sum = v4i{0, 0, 0, 0};
+    for (int sp = 0; sp < S; sp++) sum += *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int64_t col = c0 + q;
+      if (col < N) {
+        const float v = epi_value<ACT>(sum[q], cs, ep.bias[col], ep.act_param);
+        ep.y[row * N + col] = v;
+        if (ep.acc_out) ep.acc_out[row * N + col] = sum[q];
+        const uint32_t k = rgmath::absmax_key(v);
+        amax = k > amax ? k : amax;
+      }
+    }
+  }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if ((threadIdx.x & 63) == 0) spread_max(ep.absmax_out, amax);
+  }
 }
 
-// Kernel choice by how many tiles of each shape fill the 256 CUs.
+static void launch_splitk_epilogue(const int32_t* ws, int S, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                                   const Epilogue& ep, hipStream_t s) {
+  int64_t blocks = (M * (Npad / 4) + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  if (blocks < 1) blocks = 1;
+#define RG_SKE(ACTV) \
+  RG_LAUNCH(splitk_epilogue_kernel<ACTV>, dim3((unsigned)blocks), dim3(256), 0, s, ws, S, M, N, Mpad, Npad, ep)
+  switch (ep.act) {
+    case rgmath::ACT_RELU: RG_SKE(rgmath::ACT_RELU); break;
+    case rgmath::ACT_SIGMOID: RG_SKE(rgmath::ACT_SIGMOID); break;
+    case rgmath::ACT_TANH: RG_SKE(rgmath::ACT_TANH); break;
+    case rgmath::ACT_GELU: RG_SKE(rgmath::ACT_GELU); break;
+    case rgmath::ACT_LEAKY_RELU: RG_SKE(rgmath::ACT_LEAKY_RELU); break;
+    case rgmath::ACT_SILU: RG_SKE(rgmath::ACT_SILU); break;
+    default: RG_SKE(rgmath::ACT_NONE); break;
+  }
+#undef RG_SKE
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM>
+static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                       int64_t Kpad, const Epilogue& ep, int splits, int32_t* ws, hipStream_t s) {
+  const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
+  const int nk = (int)(Kpad / big::BK);
+  const int ks = (nk + splits - 1) / splits;
+  RG_LAUNCH((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM>), dim3((unsigned)(tm * tn), (unsigned)splits),
+            dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep, ks, ws);
+}
+
+// Kernel choice.  Problems with at least 256 tiles of 256 x 256 (or 256 x 128)
+// fill the CUs with the large kernels; smaller ones use 128 x 128 tiles and,
+// below 128 tiles (fewer than half the CUs busy), split K over up to 512
+// blocks of at least 4 K steps each through the workspace.
+struct GemmChoice {
+  int kind;    // 0: 256x256, 1: 256x128, 2: 128x128
+  int splits;  // K splits (128x128 only)
+};
+
+static GemmChoice choose_gemm(int64_t Mpad, int64_t Npad, int64_t Kpad) {
+  if (Mpad % 256 == 0 && Npad % 256 == 0 && (Mpad / 256) * (Npad / 256) >= 256) return {0, 1};
+  if (Mpad % 256 == 0 && Npad % 128 == 0 && (Mpad / 256) * (Npad / 128) >= 256) return {1, 1};
+  const int64_t tiles = (Mpad / 128) * (Npad / 128), nk = Kpad / big::BK;
+  if (tiles >= 128) return {2, 1};
+  int64_t S = 512 / (tiles > 0 ? tiles : 1);
+  if (S > nk / 4) S = nk / 4;
+  if (S < 1) S = 1;
+  const int64_t ks = (nk + S - 1) / S;
+  return {2, (int)((nk + ks - 1) / ks)};
+}
+
+int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad) {
+  const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
+  return g.kind == 2 && g.splits > 1 ? (int64_t)g.splits * Mpad * Npad * 4 : 0;
+}
+
 void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
-                 const Epilogue& ep, hipStream_t s) {
-  const bool kok = Kpad % big::BK == 0;
-  if (kok && Mpad % 256 == 0 && Npad % 256 == 0 && (Mpad / 256) * (Npad / 256) >= 256) {
-    launch_big<256, 256, 2, 4, 4, 1>(A, B, M, N, Mpad, Npad, Kpad, ep, s);
-    return;
+                 const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
+  if (Kpad % big::BK || Mpad % 128 || Npad % 128 || Kpad <= 0)
+    throw std::logic_error("GEMM operands must be padded to 128 rows and 64-byte K steps");
+  const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
+  if (g.kind == 0) {
+    launch_big<256, 256, 2, 4, 4, 1, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+  } else if (g.kind == 1) {
+    launch_big<256, 128, 2, 2, 3, 2, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+  } else if (g.splits > 1 && ws && ws_bytes >= (int64_t)g.splits * Mpad * Npad * 4) {
+    launch_big<128, 128, 2, 2, 4, 2, 4>(A, B, M, N, Mpad, Npad, Kpad, ep, g.splits, ws, s);
+    launch_splitk_epilogue(ws, g.splits, M, N, Mpad, Npad, ep, s);
+  } else {
+    launch_big<128, 128, 2, 2, 4, 2, 4>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   }
-  if (kok && Mpad % 256 == 0 && Npad % 128 == 0 && (Mpad / 256) * (Npad / 128) >= 256) {
-    launch_big<256, 128, 2, 2, 3, 2>(A, B, M, N, Mpad, Npad, Kpad, ep, s);
-    return;
-  }
-  constexpr int TM = 128, TN = 128;
-  dim3 grid((unsigned)(Npad / TN), (unsigned)(Mpad / TM));
-  RG_LAUNCH((gemm_i8_kernel<TM, TN>), grid, dim3(256), 0, s, A, B, M, N, Kpad, ep);
 }
 
 // ---------------------------------------------------------------------------

@@ -130,6 +130,8 @@ struct Plan {
   size_t f32_elems = 0, q_bytes = 0;
   int64_t n_slots = 0;
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
+  DevBuf ws;  // split-K partial sums
+  int64_t ws_bytes = 0;
   std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
   bool capture_ready = false;
   // Per op, indices into the run's launch events (-1 = the run-start event):
@@ -528,6 +530,8 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         pl.explicit_absmax = false;
       }
     }
+    if (op.kind == OP_LINEAR && !pl.gemv)
+      plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, op.Kpad));
     size_t qb = op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len;
     plan->q_bytes = std::max(plan->q_bytes, qb);
   }
@@ -536,6 +540,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   plan->f32[0].ensure(plan->f32_elems * sizeof(float));
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
   plan->q.ensure(plan->q_bytes);
+  if (plan->ws_bytes > 0) plan->ws.ensure((size_t)plan->ws_bytes);
   plan->slots.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(uint32_t));
   plan->scales.ensure((size_t)std::max<int64_t>(n_scales, 1) * sizeof(float));
   plan->masks.ensure(std::max<size_t>(mask_host.size(), 1));
@@ -664,7 +669,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           if (pl.gemv)
             launch_gemv(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
           else
-            launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, s);
+            launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                        plan.ws.as<int32_t>(), plan.ws_bytes, s);
         }
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
         break;

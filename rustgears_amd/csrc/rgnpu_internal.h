@@ -68,9 +68,14 @@ void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64
 void launch_quant_images(const float* x, int64_t per_img, int64_t n_img, const uint32_t* slots,
                          int8_t* q, float* scales_out, hipStream_t s);
 
-// C[M,N] = A[Mpad,Kpad] . B[Npad,Kpad]^T with the fused epilogue.
+// C[M,N] = A[Mpad,Kpad] . B[Npad,Kpad]^T with the fused epilogue.  Mpad and
+// Npad are multiples of 128, Kpad of 64.  Shapes with few tiles split K
+// through `ws` (i32 partial sums, gemm_workspace_bytes() bytes); without a
+// large enough workspace they run unsplit.
 void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad,
-                 int64_t Npad, int64_t Kpad, const Epilogue& ep, hipStream_t s);
+                 int64_t Npad, int64_t Kpad, const Epilogue& ep, int32_t* ws, int64_t ws_bytes,
+                 hipStream_t s);
+int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad);
 
 // Same contract for M <= 8 rows (weight-streaming GEMV).
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
