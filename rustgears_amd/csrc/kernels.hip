@@ -921,15 +921,27 @@ void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, in
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
+  // (R, U) from a sweep on the decode shapes (8192 x 28672 and 28672 x
+  // 8192): more rows share each activation load as M grows; long K rows
+  // favour 8 rows per wave.
+  const bool long_k = Kpad >= 16384;
   switch (M) {
     case 1: launch_gemv_t<1, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
     case 2: launch_gemv_t<2, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 3: launch_gemv_t<3, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 4: launch_gemv_t<4, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 5: launch_gemv_t<5, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 6: launch_gemv_t<6, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 7: launch_gemv_t<7, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    default: launch_gemv_t<8, 4, 2>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 3: launch_gemv_t<3, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 4: launch_gemv_t<4, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 5:
+      long_k ? launch_gemv_t<5, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<5, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      break;
+    case 6:
+      long_k ? launch_gemv_t<6, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<6, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      break;
+    case 7:
+      long_k ? launch_gemv_t<7, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<7, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      break;
+    default:
+      long_k ? launch_gemv_t<8, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<8, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      break;
   }
 }
 
