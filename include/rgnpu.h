@@ -120,9 +120,10 @@ int rgnpu_program_synchronize(rgnpu_program* prog);
 
 /* Throughput measurement on device buffers: enqueues `iters` runs back to
  * back on the program's stream, bracketed by two HIP events, waits, and
- * returns the elapsed device time.  With per_kernel_events, every kernel of
- * every run records the completion timestamp of its own dispatch (no marker
- * packets, so the region is not perturbed) and avg[i] receives op i's mean
+ * returns the elapsed device time.  Without per_kernel_events the runs record
+ * no events of their own.  With it, each run also records a start and an end
+ * marker, every kernel of every run records the completion timestamp of its
+ * own dispatch (no marker packet per kernel), and avg[i] receives op i's mean
  * op time (ns, from the previous kernel's completion to its last kernel's)
  * and main-kernel time (kernel_ns) over the iterations.  No counterpart in
  * the reference; this is the bench harness's timed region. */

@@ -159,7 +159,7 @@ RG_HD float tanhf_fdlibm(float x) {
 // their denominator.  On the GPU the correctly rounded division is
 // computed as q0 = n*rcp(d), q = fma(fma(-d, q0, n), rcp(d), q0); the
 // exhaustive device check in tests/support/devmath_gpu_check.hip confirms
-// gelu_fast == gelu and tanhf_fast == tanhf_fdlibm for all 2^32 inputs.  On
+// tanhf_fast == tanhf_fdlibm for all 2^32 inputs.  On
 // the host the division is the IEEE one, so the host build of these
 // functions is compared with glibc by tests/support/devmath_host_check.cpp.
 // ---------------------------------------------------------------------------
@@ -253,13 +253,83 @@ RG_HD float tanhf_fast(float x) {
   return ix > 0x7f800000u ? x + x : r;             // NaN
 }
 
+// GELU for the GEMM epilogues: the same f32 roundings as gelu() (fdlibm
+// tanhf over fdlibm expm1f), restricted to the arguments GELU produces and
+// with every case that cannot change the result folded away:
+//  * |u| >= 9.25: fdlibm returns z = 1 - 2/(t+2) with t + 2 >= 2^26, which
+//    rounds to 1; capping expm1's argument 2|u| at 18.5 keeps t + 2 above
+//    2^26, so the general path also yields exactly 1 (this covers fdlibm's
+//    |u| >= 22 and +-inf exits too);
+//  * |u| < 2^-55 (fdlibm's u*(1+u)) and |arg| < 2^-25 (expm1's x exit):
+//    the polynomial path returns the same value to within half an ulp of 1,
+//    which 1 + t absorbs;
+//  * expm1's k selection: k = 0 below 0.5 ln2 comes out of the rounded
+//    reduction except at its boundary, where the result is unchanged;
+//  * expm1's reconstruction for k <= -2 and for 3 <= k <= 27 is one formula
+//    y = T - (e - x), y * 2^k, minus 1 when k < 0 (T = 1 or 1 - 2^-k); the
+//    23 <= k form x - (e + 2^-k) + 1 gives the same GELU.
+// The exhaustive device check (every f32 input) confirms gelu_fast == gelu.
 RG_HD float gelu_fast(float x) {
   float x3 = 0.044715f * x; x3 = x3 * x; x3 = x3 * x;
   const float inner = x + x3;
   const float u = 0.7978846f * inner;
-  const float t = tanhf_fast(u);
+  const uint32_t ju = fbits(u), iu = ju & 0x7fffffffu;
+  const bool ge1 = iu >= 0x3f800000u;
+  const float two_au = 2.0f * bitsf(iu);
+  // tanhf: t = expm1(2|u|) for |u| >= 1, expm1(-2|u|) below
+  const float arg = ge1 ? __builtin_fminf(two_au, 18.5f) : -two_au;
+  const float ln2_hi = bitsf(0x3f317180u), ln2_lo = bitsf(0x3717f7d1u), invln2 = bitsf(0x3fb8aa3bu);
+  const float Q1 = bitsf(0xbd088889u), Q2 = bitsf(0x3ad00d01u), Q3 = bitsf(0xb8a670cdu),
+              Q4 = bitsf(0x36867e54u), Q5 = bitsf(0xb457edbbu);
+  const uint32_t hx = fbits(arg) & 0x7fffffffu;
+  float kf = invln2 * arg;
+  kf = kf + (ge1 ? 0.5f : -0.5f);
+  const int32_t k = (int32_t)kf;
+  const float tk = (float)k;
+  const float th = tk * ln2_hi;
+  const float hi = arg - th;
+  const float lo = tk * ln2_lo;
+  const float xr = hi - lo;
+  const float c = (hi - xr) - lo;
+  const float hfx = 0.5f * xr;
+  const float hxs = xr * hfx;
+  float p = hxs * Q5; p = Q4 + p;
+  p = hxs * p; p = Q3 + p;
+  p = hxs * p; p = Q2 + p;
+  p = hxs * p; p = Q1 + p;
+  p = hxs * p;
+  const float r1 = 1.0f + p;
+  const float rh = r1 * hfx;
+  const float tt = 3.0f - rh;
+  const float xt = xr * tt;
+  const float den = 6.0f - xt;
+  const float num = r1 - tt;
+  const float e = hxs * div_fast(num, den);
+  // k == 0
+  const float xe = xr * e;
+  const float r0 = xr - (xe - hxs);
+  // k != 0: e2 = x*(e-c) - c - hxs
+  const float ec = e - c;
+  float e2 = xr * ec;
+  e2 = e2 - c;
+  e2 = e2 - hxs;
+  const float em = e2 - xr;
+  // k == -1
+  const float d1 = xr - e2;
+  const float rm1 = 0.5f * d1 - 0.5f;
+  // k <= -2 and 3 <= k <= 27
+  const float T = k < 0 ? 1.0f : bitsf(0x3f800000u - (0x1000000u >> (k & 31)));
+  const float y = T - em;
+  const float ys = bitsf(fbits(y) + ((uint32_t)k << 23));
+  const float rk = k < 0 ? ys - 1.0f : ys;
+  const float t = k == 0 ? r0 : (k == -1 ? rm1 : rk);
+  // tanhf: z = 1 - 2/(t+2) for |u| >= 1, -t/(t+2) below; sign of u
+  const float d = t + 2.0f;
+  const float q = div_fast(ge1 ? 2.0f : -t, d);
+  const float z = ge1 ? 1.0f - q : q;
+  const float tanh_u = bitsf(fbits(z) ^ (ju & 0x80000000u));
   const float h = 0.5f * x;
-  const float one_t = 1.0f + t;
+  const float one_t = 1.0f + tanh_u;
   return h * one_t;
 }
 

@@ -620,18 +620,20 @@ static void op_times(const rgnpu_program* P, const Plan& plan, const hipEvent_t*
 }
 
 // Enqueue one run; x and y are device pointers.  `ev` is one run's event set
-// (events_per_run): [0] and [1] are always recorded; with `timed` every kernel
-// also records its launch event and plan.roles says which ones bound each op.
+// (events_per_run): [0] and [1] are recorded when it is given; with `timed`
+// every kernel also records its launch event and plan.roles says which ones
+// bound each op.  A null `ev` records nothing (back-to-back throughput runs).
 static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipEvent_t* ev, bool timed) {
   hipStream_t s = P->stream;
   const bool cap = P->capture;
   struct SinkOff {
     ~SinkOff() { set_launch_events(nullptr, 0); }
   } sink_off;
+  timed = timed && ev;
   set_launch_events(timed ? ev + 2 : nullptr, timed ? (int)launch_event_cap(P) : 0);
   if (cap) ensure_capture_buffers(P, plan);
   plan.roles.assign(P->ops.size(), std::array<int, 3>{-1, -1, -1});
-  RG_HIP(hipEventRecord(ev[0], s));
+  if (ev) RG_HIP(hipEventRecord(ev[0], s));
   uint32_t* slots = plan.slots.as<uint32_t>();
   float* scales = plan.scales.as<float>();
   int8_t* q = plan.q.as<int8_t>();
@@ -735,7 +737,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
   for (auto& o : P->ops) any |= o->kind != OP_FLATTEN;
   if (!any && plan.out_len > 0)
     RG_HIP(hipMemcpyAsync(y, x, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToDevice, s));
-  RG_HIP(hipEventRecord(ev[1], s));
+  if (ev) RG_HIP(hipEventRecord(ev[1], s));
   P->capture_valid = cap;
 }
 
@@ -914,7 +916,7 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
   RG_HIP(hipStreamSynchronize(P->stream));
   RG_HIP(hipEventRecord(t0, P->stream));
   for (int32_t it = 0; it < iters; it++) {
-    hipEvent_t* set = evs.data() + (per_kernel_events ? per * (size_t)it : 0);
+    hipEvent_t* set = per_kernel_events ? evs.data() + per * (size_t)it : nullptr;
     enqueue(P, plan, d_x, d_y, set, per_kernel_events != 0);
   }
   RG_HIP(hipEventRecord(t1, P->stream));
