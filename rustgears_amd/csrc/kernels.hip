@@ -147,8 +147,19 @@ __device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot, boo
   }
 }
 
+// Zeroes the other run's slot set (the plan's slots are double-buffered by
+// run parity and the first kernel of a run clears the set the next run
+// uses).  Every thread of the grid takes a share.
+__device__ __forceinline__ void clear_slots(const SlotClear& c) {
+  if (!c.p) return;
+  const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < c.n; i += nthreads)
+    c.p[i] = 0u;
+}
+
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int64_t per_img,
-                                                     uint32_t* __restrict__ slots, int spread) {
+                                                     uint32_t* __restrict__ slots, int spread, SlotClear clear) {
+  clear_slots(clear);
   const int64_t img = blockIdx.y;
   const float* xi = x + img * per_img;
   uint32_t m = 0;
@@ -177,7 +188,9 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
 __global__ __launch_bounds__(256) void absmax_masked_kernel(const float* __restrict__ x, int64_t per_img,
                                                             uint32_t* __restrict__ slots,
                                                             const uint8_t* __restrict__ rowmask,
-                                                            const uint8_t* __restrict__ colmask, int H, int W) {
+                                                            const uint8_t* __restrict__ colmask, int H, int W,
+                                                            SlotClear clear) {
+  clear_slots(clear);
   const int64_t img = blockIdx.y;
   const float* xi = x + img * per_img;
   uint32_t m = 0;
@@ -194,7 +207,8 @@ __global__ __launch_bounds__(256) void absmax_masked_kernel(const float* __restr
 }
 
 void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, bool spread,
-                   const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W, hipStream_t s) {
+                   const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W, hipStream_t s,
+                   SlotClear clear) {
   if (per_img <= 0 || n_img <= 0) return;
   if (spread && (n_img != 1 || rowmask)) throw std::logic_error("spread absmax takes one unmasked tensor");
   int64_t bx = (per_img + 256 * 16 - 1) / (256 * 16);
@@ -203,10 +217,10 @@ void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slo
   if (bx < 1) bx = 1;
   if (rowmask)
     RG_LAUNCH(absmax_masked_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
-                       rowmask, colmask, (int)H, (int)W);
+                       rowmask, colmask, (int)H, (int)W, clear);
   else
     RG_LAUNCH(absmax_kernel, dim3((unsigned)bx, (unsigned)n_img), dim3(256), 0, s, x, per_img, slots,
-                       spread ? 1 : 0);
+                       spread ? 1 : 0, clear);
 }
 
 // ---------------------------------------------------------------------------

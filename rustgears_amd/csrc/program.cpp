@@ -129,6 +129,13 @@ struct Plan {
   std::vector<OpPlan> ops;
   size_t f32_elems = 0, q_bytes = 0;
   int64_t n_slots = 0;
+  // Slot sets: with clear_by_first the slots are two sets of n_slots words;
+  // run k uses set `parity` and its first kernel (the input absmax) zeroes
+  // the other one for run k + 1.  Otherwise one set, filled with zeros at
+  // the start of every run.
+  bool clear_by_first = false;
+  int parity = 0;
+  int64_t slot_set_words = 0;  // n_slots rounded up to a 128-byte multiple
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
   DevBuf ws;  // split-K partial sums
   int64_t ws_bytes = 0;
@@ -536,12 +543,25 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     plan->q_bytes = std::max(plan->q_bytes, qb);
   }
   plan->n_slots = slots;
+  // The first computing op quantizes the input itself (its absmax is the
+  // run's first kernel) unless the input is empty.
+  for (size_t i = 0; i < nops; i++) {
+    const Op& op = *P->ops[i];
+    if (op.kind == OP_FLATTEN) continue;
+    const OpPlan& pl = plan->ops[i];
+    plan->clear_by_first =
+        slots > 0 && (op.kind == OP_LINEAR || op.kind == OP_CONV) && pl.explicit_absmax && pl.in_len > 0;
+    break;
+  }
 
   plan->f32[0].ensure(plan->f32_elems * sizeof(float));
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
   plan->q.ensure(plan->q_bytes);
   if (plan->ws_bytes > 0) plan->ws.ensure((size_t)plan->ws_bytes);
-  plan->slots.ensure((size_t)std::max<int64_t>(slots, 1) * sizeof(uint32_t));
+  plan->slot_set_words = round_up(std::max<int64_t>(slots, 1), kSpreadStride);
+  const size_t slot_bytes = (size_t)plan->slot_set_words * sizeof(uint32_t) * (plan->clear_by_first ? 2 : 1);
+  plan->slots.ensure(slot_bytes);
+  RG_HIP(hipMemsetAsync(plan->slots.p, 0, slot_bytes, P->stream));
   plan->scales.ensure((size_t)std::max<int64_t>(n_scales, 1) * sizeof(float));
   plan->masks.ensure(std::max<size_t>(mask_host.size(), 1));
   if (!mask_host.empty())
@@ -634,10 +654,25 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
   if (cap) ensure_capture_buffers(P, plan);
   plan.roles.assign(P->ops.size(), std::array<int, 3>{-1, -1, -1});
   if (ev) RG_HIP(hipEventRecord(ev[0], s));
-  uint32_t* slots = plan.slots.as<uint32_t>();
+  uint32_t* const slot_sets = plan.slots.as<uint32_t>();
+  uint32_t* slots = slot_sets;
+  SlotClear clear{};  // handed to the run's first kernel, then reset
+  if (plan.clear_by_first) {
+    slots = slot_sets + plan.parity * plan.slot_set_words;
+    clear = SlotClear{slot_sets + (1 - plan.parity) * plan.slot_set_words, plan.n_slots};
+  } else if (plan.n_slots > 0) {
+    launch_fill_u32(slots, plan.n_slots, 0u, s);
+  }
+  // The other set is zero once the first kernel is enqueued: from then on
+  // the next run uses it, whatever happens later in this one.
+  auto first_launched = [&]() {
+    if (clear.p) {
+      clear = SlotClear{};
+      plan.parity ^= 1;
+    }
+  };
   float* scales = plan.scales.as<float>();
   int8_t* q = plan.q.as<int8_t>();
-  if (plan.n_slots > 0) launch_fill_u32(slots, plan.n_slots, 0u, s);
   auto buf = [&](int id) -> float* {
     if (id == BUF_INPUT) return const_cast<float*>(x);
     if (id == BUF_OUTPUT) return y;
@@ -654,7 +689,10 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     switch (op.kind) {
       case OP_LINEAR: {
         uint32_t* slot = slots + pl.slot_base;
-        if (pl.explicit_absmax) launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s);
+        if (pl.explicit_absmax) {
+          launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s, clear);
+          first_launched();
+        }
         launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, q, scales + pl.scale_base, s);
         Epilogue ep;
         ep.bias = op.d_bias.as<float>();
@@ -684,9 +722,10 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         if (pl.explicit_absmax) {
           const uint8_t* mk = plan.masks.as<uint8_t>() + pl.mask_off;
           if (pl.full_cov)
-            launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s);
+            launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s, clear);
           else
-            launch_absmax(in, per, c.n, sl, false, mk, mk + c.H, c.H, c.W, s);
+            launch_absmax(in, per, c.n, sl, false, mk, mk + c.H, c.H, c.W, s, clear);
+          first_launched();
         }
         launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
         Epilogue ep;

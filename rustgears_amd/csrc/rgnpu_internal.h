@@ -26,6 +26,14 @@ constexpr int kSpread = 64;
 constexpr int kSpreadStride = 32;
 constexpr int64_t kTensorSlotWords = (int64_t)kSpread * kSpreadStride;
 
+// A plan's absmax slots are double-buffered by run parity when the run's
+// first kernel is an input absmax: that kernel also zeroes the other set
+// (p[0 .. n)), which the next run then uses.
+struct SlotClear {
+  uint32_t* p = nullptr;
+  int64_t n = 0;
+};
+
 // Fused epilogue parameters: y = act(float(acc) * (sa * sw) + bias[n]).
 struct Epilogue {
   const float* bias = nullptr;        // [N] (padded)
@@ -57,7 +65,8 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 // which (row, col) positions of a [C,H,W] image participate.
 void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slots, bool spread,
                    const uint8_t* rowmask, const uint8_t* colmask, int64_t H, int64_t W,
-                   hipStream_t s);
+                   hipStream_t s,
+                   SlotClear clear = SlotClear{});
 
 // x f32 [M,K] -> q i8 [Mpad,Kpad] (zero padded), scale from a spread slot.
 // scale_out (nullable) receives the scale used.

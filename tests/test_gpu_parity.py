@@ -254,6 +254,37 @@ def test_device_resident_run_matches_host_run(rg, ref):
     assert sess.last_npu_profile().total_time_ns > 0
 
 
+@pytest.mark.parametrize("kind", ["linear_small", "linear_large", "conv_first", "pool_first"])
+def test_consecutive_runs_on_one_session(rg, ref, kind):
+    """Several runs of one session with alternating input magnitudes: the
+    absmax slots are reused run after run (double-buffered, cleared by each
+    run's first kernel, or zero-filled), so a stale larger absmax would show
+    up as a wrong scale in a later, smaller run."""
+    from rustgears_amd import nn
+    rg.manual_seed(23)
+    if kind == "linear_small":  # GEMV path
+        model = nn.Sequential().add(nn.Linear(512, 256)).add(nn.Tanh()).add(nn.Linear(256, 64))
+        shape = [4, 512]
+    elif kind == "linear_large":
+        model = nn.Sequential().add(nn.Linear(300, 256)).add(nn.Relu()).add(nn.Linear(256, 32))
+        shape = [700, 300]
+    elif kind == "conv_first":
+        model = (nn.Sequential().add(nn.Conv2d(3, 8, 3).padding(1)).add(nn.Relu()).add(nn.MaxPool2d(2))
+                 .add(nn.Flatten()).add(nn.Linear(8 * 4 * 4, 10)))
+        shape = [6, 3, 8, 8]
+    else:  # first kernel is a max pool: the slots are zero-filled each run
+        model = nn.Sequential().add(nn.MaxPool2d(2)).add(nn.Conv2d(3, 4, 3)).add(nn.Flatten()).add(nn.Linear(4 * 2 * 2, 5))
+        shape = [5, 3, 8, 8]
+    layers = model.export()
+    sess = make_session(rg, layers)
+    p = ref.RefProgram(layers)
+    for i, mag in enumerate([50.0, 0.01, 3.0, 1e-3, 200.0]):
+        print(f"[parity] consecutive {kind} run {i} magnitude {mag}", flush=True)
+        x = (rg.randn(shape) * mag).astype(np.float32)
+        assert_bitexact_f32(sess.run(x), p.run(x), f"{kind} run {i}")
+    sess.close()
+
+
 def test_compilation_report(rg, ref):
     from rustgears_amd import nn
     rg.manual_seed(0)
