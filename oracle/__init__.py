@@ -82,6 +82,10 @@ def lib() -> ctypes.CDLL:
             ("rgref_max_pool2d", None, [f32p] + [ctypes.c_int64] * 6 + [f32p, ctypes.c_int]),
             ("rgref_softmax_rows", None, [f32p, ctypes.c_int64, ctypes.c_int64, f32p]),
             ("rgref_compile", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64]),
+            ("rgref_compile_precision", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64, ctypes.c_int]),
+            ("rgref_round_fp16", ctypes.c_float, [ctypes.c_float]),
+            ("rgref_fp16_gemm_fused", None, [f32p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, f32p,
+                                             ctypes.c_int, ctypes.c_float, f32p, ctypes.c_int]),
             ("rgref_program_free", None, [ctypes.c_void_p]),
             ("rgref_program_num_ops", ctypes.c_int64, [ctypes.c_void_p]),
             ("rgref_program_fp32_bytes", ctypes.c_int64, [ctypes.c_void_p]),
@@ -223,12 +227,37 @@ def to_ref_layers(layers: Sequence) -> tuple:
     return arr, keep
 
 
-class RefProgram:
-    """npu::compile + NpuProgram::execute restated on the CPU."""
+INT8, FP16 = 0, 1  # NpuPrecision (npu.rs:25-30)
 
-    def __init__(self, layers: Sequence):
+
+def round_fp16(x) -> np.ndarray:
+    """round_fp16 (quantize.rs:50-64), elementwise."""
+    a = np.ascontiguousarray(np.asarray(x, np.float32))
+    f = lib().rgref_round_fp16
+    return np.array([f(float(v)) for v in a.ravel()], np.float32).reshape(a.shape)
+
+
+def fp16_gemm_fused(a, b_t, bias, act: int = 0, param: float = 0.0) -> np.ndarray:
+    """fp16_gemm_fused (npu.rs:425-445): a [m,k] f32, b_t [n,k] f32 (already
+    fp16-rounded), bias [n]."""
+    a = np.ascontiguousarray(a, np.float32)
+    b_t = np.ascontiguousarray(b_t, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    m, k = a.shape
+    n = b_t.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().rgref_fp16_gemm_fused(_fp(a), _fp(b_t), m, k, n, _fp(bias), act, param, _fp(out), 0)
+    return out
+
+
+class RefProgram:
+    """npu::compile + NpuProgram::execute restated on the CPU, for
+    NpuPrecision::Int8 (precision=INT8) or ::Fp16 (precision=FP16)."""
+
+    def __init__(self, layers: Sequence, precision: int = INT8):
         arr, keep = to_ref_layers(layers)
-        self._p = lib().rgref_compile(arr, len(layers))
+        self._p = lib().rgref_compile_precision(arr, len(layers), precision)
+        self.precision = precision
         del keep
 
     def __del__(self):

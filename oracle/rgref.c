@@ -116,6 +116,24 @@ float rgref_quantize(const float* v, int64_t n, int8_t* out) {
   return scale;
 }
 
+/* round_fp16 (quantize.rs:50-64): keeps the top 10 mantissa bits after
+ * adding half an ulp to the magnitude (ties round up, not to even),
+ * flushes exponents below -14 to +0 (the sign is dropped) and clamps
+ * exponents above 15 to +-65504 (NaN and +-inf included, with their sign
+ * bit).  The exponent is read before rounding, so [65520, 65536) rounds to
+ * 65536. */
+float rgref_round_fp16(float x) {
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  const uint32_t sign = bits & 0x80000000u;
+  const int32_t e = (int32_t)((bits >> 23) & 0xffu) - 127;
+  if (e < -14) return 0.0f;
+  uint32_t r = e > 15 ? (sign | 0x477fe000u) : ((bits + (1u << 12)) & ~0x1fffu);
+  float y;
+  memcpy(&y, &r, 4);
+  return y;
+}
+
 /* dot_i8 (quantize.rs:68-88): four i32 lanes then a tail.  i32 adds wrap in
  * release Rust; the order only matters on overflow, where wrapping sums are
  * still order-independent. */
@@ -143,6 +161,34 @@ static void gemm_row(const int8_t* arow, const int8_t* b_t, int64_t k, int64_t n
     orow[c] = rgref_act_apply(act, p, val);
   }
 }
+/* fp16_gemm_fused_into (npu.rs:433-445): each output is a serial f32 sum,
+ * k ascending, of round_fp16(a) * w (multiply then add, no FMA), then
+ * act(round_fp16(acc + bias[c])).  The reference runs rows serially; rows
+ * are independent, so the optional row-parallel loop gives the same bits. */
+static void fp16_gemm_row(const float* arow, const float* b_t, int64_t k, int64_t n, const float* bias, int act,
+                          float p, float* orow, float* ah) {
+  for (int64_t j = 0; j < k; j++) ah[j] = rgref_round_fp16(arow[j]);
+  for (int64_t c = 0; c < n; c++) {
+    const float* brow = b_t + c * k;
+    float acc = 0.0f;
+    for (int64_t j = 0; j < k; j++) {
+      float prod = ah[j] * brow[j];
+      acc = acc + prod;
+    }
+    float t = acc + bias[c];
+    orow[c] = rgref_act_apply(act, p, rgref_round_fp16(t));
+  }
+}
+void rgref_fp16_gemm_fused(const float* a, const float* b_t, int64_t m, int64_t k, int64_t n, const float* bias,
+                           int act, float p, float* out, int parallel) {
+#pragma omp parallel for schedule(dynamic, 4) num_threads(rgref_get_threads()) if (parallel && m * k * n >= 32 * 1024)
+  for (int64_t r = 0; r < m; r++) {
+    float* ah = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+    fp16_gemm_row(a + r * k, b_t, k, n, bias, act, p, out + r * n, ah);
+    free(ah);
+  }
+}
+
 /* int8_gemm_fused (quantize.rs:93-118) / int8_gemm_fused_serial (122-144).
  * The parallel split is over output rows when m*k*n >= 32768 (quantize.rs:104). */
 void rgref_int8_gemm_fused(const int8_t* a, float a_scale, const int8_t* b_t, float b_scale,
@@ -242,6 +288,7 @@ typedef struct {
   int64_t in_f, out_f;              /* Linear: in/out features; Conv: in/out channels */
   int64_t kernel, stride, padding;
   int8_t* wq; float w_scale; int64_t w_len;
+  float* wh;  /* FP16: round_fp16 weights [out, in] / [out, c*k*k]; the raw diagonal for a lone ChannelAffine */
   float* bias;
   int act; float act_param;
   /* captures */
@@ -253,6 +300,7 @@ typedef struct {
 } ref_op;
 
 struct rgref_program {
+  int precision; /* RGREF_INT8 or RGREF_FP16 (NpuPrecision, npu.rs:25-30) */
   ref_op* ops; int64_t n_ops;
   int64_t original_layers, fp32_bytes, npu_bytes;
   int capture;
@@ -325,10 +373,21 @@ static void free_folded(folded_layer* f, int64_t n) {
   free(f);
 }
 
+static float* round_fp16_copy(const float* w, int64_t n) {
+  float* r = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+  for (int64_t i = 0; i < n; i++) r[i] = rgref_round_fp16(w[i]);
+  return r;
+}
+
 rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers) {
+  return rgref_compile_precision(layers, n_layers, RGREF_INT8);
+}
+
+rgref_program* rgref_compile_precision(const rgref_layer* layers, int64_t n_layers, int precision) {
   int64_t nf = 0;
   folded_layer* F = fold_batch_norm(layers, n_layers, &nf);
   rgref_program* P = (rgref_program*)calloc(1, sizeof(rgref_program));
+  P->precision = precision;
   P->ops = (ref_op*)calloc((size_t)(nf > 0 ? nf : 1), sizeof(ref_op));
   P->original_layers = n_layers;
   int64_t i = 0;
@@ -349,10 +408,11 @@ rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers) {
       op->w_len = f->in_f * f->out_f;
       op->wq = (int8_t*)malloc((size_t)(op->w_len > 0 ? op->w_len : 1));
       op->w_scale = rgref_quantize(wt, op->w_len, op->wq);
+      op->wh = round_fp16_copy(wt, op->w_len); /* npu.rs:210 */
       free(wt);
       op->bias = dupf(f->b, f->b_len);
       P->fp32_bytes += (f->w_len + f->b_len) * 4;
-      P->npu_bytes += (op->w_len + 4) + f->b_len * 4;
+      P->npu_bytes += precision == RGREF_FP16 ? f->w_len * 2 + f->b_len * 2 : (op->w_len + 4) + f->b_len * 4;
       P->n_ops++;
     } else if (f->kind == RGREF_CONV2D) {
       op->kind = RGREF_CONV2D;
@@ -364,9 +424,10 @@ rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers) {
       op->w_len = f->w_len;
       op->wq = (int8_t*)malloc((size_t)(op->w_len > 0 ? op->w_len : 1));
       op->w_scale = rgref_quantize(f->w, op->w_len, op->wq); /* [out, c*k*k] (npu.rs:231) */
+      op->wh = round_fp16_copy(f->w, op->w_len);             /* npu.rs:232 */
       op->bias = dupf(f->b, f->b_len);
       P->fp32_bytes += (f->w_len + f->b_len) * 4;
-      P->npu_bytes += (op->w_len + 4) + f->b_len * 4;
+      P->npu_bytes += precision == RGREF_FP16 ? f->w_len * 2 + f->b_len * 2 : (op->w_len + 4) + f->b_len * 4;
       P->n_ops++;
     } else if (f->kind == RGREF_CHANNEL_AFFINE) {
       /* lone ChannelAffine -> diagonal FusedLinear, no byte accounting (npu.rs:254-270) */
@@ -377,7 +438,7 @@ rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers) {
       op->w_len = c * c;
       op->wq = (int8_t*)malloc((size_t)(op->w_len > 0 ? op->w_len : 1));
       op->w_scale = rgref_quantize(w, op->w_len, op->wq);
-      free(w);
+      op->wh = w; /* weight_fp16_t: w as is, not rounded (npu.rs:266) */
       op->bias = dupf(f->shift, c);
       P->n_ops++;
     } else {
@@ -400,7 +461,9 @@ static void free_caps(ref_op* op) {
 
 void rgref_program_free(rgref_program* p) {
   if (!p) return;
-  for (int64_t i = 0; i < p->n_ops; i++) { free(p->ops[i].wq); free(p->ops[i].bias); free_caps(&p->ops[i]); }
+  for (int64_t i = 0; i < p->n_ops; i++) {
+    free(p->ops[i].wq); free(p->ops[i].wh); free(p->ops[i].bias); free_caps(&p->ops[i]);
+  }
   free(p->ops); free(p->out); free(p);
 }
 int64_t rgref_program_num_ops(const rgref_program* p) { return p->n_ops; }
@@ -533,6 +596,13 @@ int rgref_execute(rgref_program* P, const float* x, const int64_t* shape_in, int
       if (in <= 0 || len % in != 0) { free(data); set_err("Linear: input length not a multiple of in_features"); return 1; }
       int64_t rows = len / in;
       op->macs = rows * in * out;
+      if (P->precision == RGREF_FP16) {                                /* npu.rs:315 */
+        float* y = (float*)xmalloc(sizeof(float) * (size_t)(rows * out));
+        rgref_fp16_gemm_fused(data, op->wh, rows, in, out, op->bias, op->act, op->act_param, y, parallel);
+        free(data); data = y; len = rows * out;
+        shape[nd - 1] = out;
+        goto op_done;
+      }
       int8_t* aq = (int8_t*)xmalloc((size_t)(rows * in));
       float sa = rgref_quantize(data, rows * in, aq);
       float* y = (float*)xmalloc(sizeof(float) * (size_t)(rows * out));
@@ -558,6 +628,22 @@ int rgref_execute(rgref_program* P, const float* x, const int64_t* shape_in, int
       int64_t l = oh * ow, ckk = c * k * k, img = c * h * w, ostr = O * l;
       op->macs = n * O * ckk * l;
       float* out = (float*)xmalloc(sizeof(float) * (size_t)(n * ostr));
+      if (P->precision == RGREF_FP16) {                                /* npu.rs:353-355, 374-376 */
+#pragma omp parallel for schedule(dynamic, 1) num_threads(rgref_get_threads()) if (parallel && n >= 2 && ostr > 0)
+        for (int64_t b = 0; b < n; b++) {
+          float* cols = (float*)xmalloc(sizeof(float) * (size_t)(ckk * l));
+          float* cols_t = (float*)xmalloc(sizeof(float) * (size_t)(l * ckk));
+          float* ylo = (float*)xmalloc(sizeof(float) * (size_t)(l * O));
+          rgref_im2col(data + b * img, c, h, w, k, s, pd, oh, ow, cols);
+          rgref_transpose2d(cols, ckk, l, cols_t);
+          rgref_fp16_gemm_fused(cols_t, op->wh, l, ckk, O, op->bias, op->act, op->act_param, ylo, 0);
+          rgref_transpose2d(ylo, l, O, out + b * ostr);
+          free(cols); free(cols_t); free(ylo);
+        }
+        free(data); data = out; len = n * ostr;
+        shape[0] = n; shape[1] = O; shape[2] = oh; shape[3] = ow; nd = 4;
+        goto op_done;
+      }
       if (P->capture) {
         op->cap_q = (int8_t*)xmalloc((size_t)(n * l * ckk)); op->cap_q_len = n * l * ckk;
         op->cap_scale = (float*)xmalloc(sizeof(float) * (size_t)n); op->cap_scale_len = n;
@@ -601,6 +687,7 @@ int rgref_execute(rgref_program* P, const float* x, const int64_t* shape_in, int
       if (last > 0) rgref_softmax_rows(data, len / last, last, y);
       free(data); data = y;
     }
+  op_done:
     if (P->capture) {
       op->cap_out = (float*)xmalloc(sizeof(float) * (size_t)len);
       memcpy(op->cap_out, data, sizeof(float) * (size_t)len);

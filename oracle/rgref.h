@@ -1,9 +1,9 @@
 /*
- * rgref — CPU oracle for the RustGears NPU INT8 inference path.
+ * rgref — CPU oracle for the RustGears NPU inference path (INT8 and FP16).
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
  * Rust code (elandice/RustGears) for `InferenceSession` with
- * `ExecutionProvider::Npu(NpuPrecision::Int8)`.  It exists to check the HIP
+ * `ExecutionProvider::Npu(NpuPrecision::Int8)` and `::Fp16`.  It exists to check the HIP
  * execution provider and to time the reference algorithm on host cores.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it; the product library never links or calls it.
@@ -87,7 +87,12 @@ void rgref_softmax_rows(const float* x, int64_t outer, int64_t size, float* y); 
 
 /* ---- compile / execute (npu.rs:188-276, 296-421) --------------------------- */
 typedef struct rgref_program rgref_program;
-rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers);
+enum { RGREF_INT8 = 0, RGREF_FP16 = 1 }; /* NpuPrecision (npu.rs:25-30) */
+float rgref_round_fp16(float x);                              /* quantize.rs:50-64 */
+void rgref_fp16_gemm_fused(const float* a, const float* b_t, int64_t m, int64_t k, int64_t n,
+                           const float* bias, int act, float p, float* out, int parallel); /* npu.rs:433-445 */
+rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers); /* INT8 */
+rgref_program* rgref_compile_precision(const rgref_layer* layers, int64_t n_layers, int precision);
 void    rgref_program_free(rgref_program* p);
 int64_t rgref_program_num_ops(const rgref_program* p);
 int64_t rgref_program_fp32_bytes(const rgref_program* p);
