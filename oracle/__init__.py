@@ -84,6 +84,9 @@ def lib() -> ctypes.CDLL:
             ("rgref_compile", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64]),
             ("rgref_compile_precision", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64, ctypes.c_int]),
             ("rgref_round_fp16", ctypes.c_float, [ctypes.c_float]),
+            ("rgref_round_fp16_array", None, [f32p, f32p, ctypes.c_int64]),
+            ("rgref_program_op_weight_fp16", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(f32p),
+                                                              i64p]),
             ("rgref_fp16_gemm_fused", None, [f32p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, f32p,
                                              ctypes.c_int, ctypes.c_float, f32p, ctypes.c_int]),
             ("rgref_program_free", None, [ctypes.c_void_p]),
@@ -233,8 +236,9 @@ INT8, FP16 = 0, 1  # NpuPrecision (npu.rs:25-30)
 def round_fp16(x) -> np.ndarray:
     """round_fp16 (quantize.rs:50-64), elementwise."""
     a = np.ascontiguousarray(np.asarray(x, np.float32))
-    f = lib().rgref_round_fp16
-    return np.array([f(float(v)) for v in a.ravel()], np.float32).reshape(a.shape)
+    y = np.empty_like(a)
+    lib().rgref_round_fp16_array(_fp(a), _fp(y), a.size)
+    return y
 
 
 def fp16_gemm_fused(a, b_t, bias, act: int = 0, param: float = 0.0) -> np.ndarray:
@@ -297,6 +301,15 @@ class RefProgram:
         if n <= 0 or not w:
             return np.zeros(0, np.int8), np.float32(s.value)
         return np.ctypeslib.as_array(w, shape=(n,)).copy(), np.float32(s.value)
+
+    def op_weight_fp16(self, i: int) -> np.ndarray:
+        """FP16 program: op i's round_fp16 weights as [out, K] f32."""
+        w = f32p()
+        rows = ctypes.c_int64()
+        n = lib().rgref_program_op_weight_fp16(self._p, i, ctypes.byref(w), ctypes.byref(rows))
+        if n <= 0 or not w:
+            return np.zeros((0, 0), np.float32)
+        return np.ctypeslib.as_array(w, shape=(n,)).copy().reshape(rows.value, n // rows.value)
 
     def set_capture(self, on: bool) -> None:
         lib().rgref_program_set_capture(self._p, 1 if on else 0)

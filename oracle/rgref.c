@@ -134,6 +134,10 @@ float rgref_round_fp16(float x) {
   return y;
 }
 
+void rgref_round_fp16_array(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) y[i] = rgref_round_fp16(x[i]);
+}
+
 /* dot_i8 (quantize.rs:68-88): four i32 lanes then a tail.  i32 adds wrap in
  * release Rust; the order only matters on overflow, where wrapping sums are
  * still order-independent. */
@@ -473,6 +477,13 @@ int64_t rgref_program_original_layers(const rgref_program* p) { return p->origin
 int64_t rgref_program_op_macs(const rgref_program* p, int64_t i) { return p->ops[i].macs; }
 int64_t rgref_program_total_macs(const rgref_program* p) { return p->total_macs; }
 void rgref_program_set_capture(rgref_program* p, int on) { p->capture = on; }
+
+int64_t rgref_program_op_weight_fp16(const rgref_program* p, int64_t i, const float** w, int64_t* rows) {
+  const ref_op* op = &p->ops[i];
+  *w = op->wh;
+  *rows = op->out_f;
+  return op->wh ? op->w_len : 0;
+}
 
 int64_t rgref_program_op_weight(const rgref_program* p, int64_t i, const int8_t** w, float* scale,
                                 const float** bias) {

@@ -89,10 +89,13 @@ void rgref_softmax_rows(const float* x, int64_t outer, int64_t size, float* y); 
 typedef struct rgref_program rgref_program;
 enum { RGREF_INT8 = 0, RGREF_FP16 = 1 }; /* NpuPrecision (npu.rs:25-30) */
 float rgref_round_fp16(float x);                              /* quantize.rs:50-64 */
+void rgref_round_fp16_array(const float* x, float* y, int64_t n);
 void rgref_fp16_gemm_fused(const float* a, const float* b_t, int64_t m, int64_t k, int64_t n,
                            const float* bias, int act, float p, float* out, int parallel); /* npu.rs:433-445 */
 rgref_program* rgref_compile(const rgref_layer* layers, int64_t n_layers); /* INT8 */
 rgref_program* rgref_compile_precision(const rgref_layer* layers, int64_t n_layers, int precision);
+/* FP16 weights of op i ([out, K] row-major, as round_fp16'd by compile); 0 when none. */
+int64_t rgref_program_op_weight_fp16(const rgref_program* p, int64_t i, const float** w, int64_t* rows);
 void    rgref_program_free(rgref_program* p);
 int64_t rgref_program_num_ops(const rgref_program* p);
 int64_t rgref_program_fp32_bytes(const rgref_program* p);

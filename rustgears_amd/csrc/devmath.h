@@ -422,6 +422,29 @@ RG_HD int8_t quantize_one(float v, float inv) {
   return (int8_t)(int)t;
 }
 
+// round_fp16 (quantize.rs:50-64): half an ulp added to the magnitude, then
+// the low 13 mantissa bits cleared (ties away from zero); exponents below
+// -14 give +0 and above 15 give +-65504 (NaN and inf included).  The
+// exponent is read before rounding, so [65520, 65536) gives 65536.
+RG_HD float round_fp16(float x) {
+  const uint32_t bits = fbits(x);
+  const int32_t e = (int32_t)((bits >> 23) & 0xffu) - 127;
+  const uint32_t r = e > 15 ? ((bits & 0x80000000u) | 0x477fe000u) : ((bits + (1u << 12)) & ~0x1fffu);
+  return e < -14 ? 0.0f : bitsf(r);
+}
+
+// IEEE binary16 bits of a round_fp16 result (exact: 10 mantissa bits and an
+// exponent in [-14, 15]), except +-65536, which binary16 cannot hold and
+// which saturates to +-65504.
+RG_HD uint16_t fp16_bits(float r) {
+  const uint32_t b = fbits(r);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const uint32_t mag = b & 0x7fffffffu;
+  if (mag == 0) return (uint16_t)sign;
+  if (mag >= 0x47800000u) return (uint16_t)(sign | 0x7bffu);
+  return (uint16_t)(sign | (((mag >> 23) - 112u) << 10) | ((mag >> 13) & 0x3ffu));
+}
+
 // |v| as an ordered integer for atomicMax; NaN is ignored (f32::max).
 RG_HD uint32_t absmax_key(float v) {
   uint32_t b = fbits(v) & 0x7fffffffu;

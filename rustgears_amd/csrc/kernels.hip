@@ -19,6 +19,8 @@
 namespace rgnpu {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 // Launch-event sink (see set_launch_events): every kernel launched while it
 // is set carries the next event as the stop event of its own dispatch.
@@ -100,6 +102,19 @@ __device__ __forceinline__ float epi_value(int32_t acc, float cs, float b, float
   const float prod = (float)acc * cs;
   const float val = prod + b;
   return act_fixed<ACT>(val, p);
+}
+
+// One accumulator word to its output.  INT8: the i32 sum, y = act(fl(float(acc)
+// * cs) + b).  FP16: the bits of the f32 sum, y = act(round_fp16(acc + b))
+// (npu.rs:442).
+template <int ACT, bool F16>
+__device__ __forceinline__ float epi_word(int32_t w, float cs, float b, float p) {
+  if constexpr (F16) {
+    const float t = __int_as_float(w) + b;
+    return act_fixed<ACT>(rgmath::round_fp16(t), p);
+  } else {
+    return epi_value<ACT>(w, cs, b, p);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -289,6 +304,136 @@ void launch_quant_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64
 }
 
 // ---------------------------------------------------------------------------
+// FP16 operands (NpuPrecision::Fp16): round_fp16 (quantize.rs:50-64) of each
+// f32 activation, stored as IEEE binary16 (exact, see rgmath::fp16_bits).
+// Rows: x [M, K] -> h [Mpad, Kpad_h], one thread per 8 halves (16 bytes),
+// zero padding.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t half2_of(float a, float b) {
+  return (uint32_t)rgmath::fp16_bits(rgmath::round_fp16(a)) | ((uint32_t)rgmath::fp16_bits(rgmath::round_fp16(b)) << 16);
+}
+
+__global__ __launch_bounds__(256) void half_rows_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                        int64_t Mpad, int64_t Kpad_h, uint16_t* __restrict__ h) {
+  const uint32_t chunks = (uint32_t)(Kpad_h / 8);
+  const int64_t total = Mpad * (int64_t)chunks;
+  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = w / chunks;
+    const uint32_t c0 = (uint32_t)(w - r * chunks) * 8u;
+    v4i out = v4i{0, 0, 0, 0};
+    if (r < M) {
+      const float* xr = x + r * K;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = c0 + (uint32_t)e < (uint32_t)K ? xr[c0 + e] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < 4; g++) out[g] = (int)half2_of(v[2 * g], v[2 * g + 1]);
+    }
+    reinterpret_cast<v4i*>(h)[w] = out;
+  }
+}
+
+void launch_half_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_h, uint16_t* h, hipStream_t s) {
+  const int64_t chunks = Mpad * (Kpad_h / 8);
+  if (chunks <= 0) return;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(half_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_h, h);
+}
+
+// im2col in binary16 for the FP16 conv (npu.rs:341-355): row img*L + oy*OW + ox,
+// column kk = (c*k + ki)*k + kj as in im2col_into (kernels.rs:28-96), value
+// round_fp16(x) or 0 for padding; rows past n*L and columns past C*k*k are 0.
+__global__ __launch_bounds__(256) void im2col_half_kernel(const float* __restrict__ x, ConvShape cs, int64_t Mpad,
+                                                          int64_t Kpad_h, uint16_t* __restrict__ h) {
+  const uint32_t k = (uint32_t)cs.k, kk2 = k * k, ckk = (uint32_t)cs.C * kk2;
+  const uint32_t L = (uint32_t)(cs.OH * cs.OW), OW = (uint32_t)cs.OW;
+  const uint32_t H = (uint32_t)cs.H, W = (uint32_t)cs.W;
+  const int64_t rows = cs.n * (int64_t)L;
+  const uint32_t chunks = (uint32_t)(Kpad_h / 8);
+  const int64_t total = Mpad * (int64_t)chunks;
+  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = w / chunks;
+    const uint32_t c0 = (uint32_t)(w - r * chunks) * 8u;
+    v4i out = v4i{0, 0, 0, 0};
+    if (r < rows) {
+      const int64_t img = r / L;
+      const uint32_t p = (uint32_t)(r - img * L);
+      const uint32_t oy = p / OW, ox = p - oy * OW;
+      const float* xi = x + img * (int64_t)(cs.C * cs.H * cs.W);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const uint32_t kk = c0 + (uint32_t)e;
+        float val = 0.0f;
+        if (kk < ckk) {
+          const uint32_t c = kk / kk2, t = kk - c * kk2, ki = t / k, kj = t - ki * k;
+          const int iy = (int)(oy * (uint32_t)cs.stride + ki) - (int)cs.pad;
+          const int ix = (int)(ox * (uint32_t)cs.stride + kj) - (int)cs.pad;
+          if (iy >= 0 && iy < (int)H && ix >= 0 && ix < (int)W) val = xi[(c * H + (uint32_t)iy) * W + (uint32_t)ix];
+        }
+        v[e] = val;
+      }
+#pragma unroll
+      for (int g = 0; g < 4; g++) out[g] = (int)half2_of(v[2 * g], v[2 * g + 1]);
+    }
+    reinterpret_cast<v4i*>(h)[w] = out;
+  }
+}
+
+void launch_im2col_half(const float* x, const ConvShape& cs, int64_t Mpad, int64_t Kpad_h, uint16_t* h,
+                        hipStream_t s) {
+  const int64_t chunks = Mpad * (Kpad_h / 8);
+  if (chunks <= 0) return;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(im2col_half_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, cs, Mpad, Kpad_h, h);
+}
+
+// y_lo [n*L, O] (row stride O) -> NCHW [n, O, L] (transpose2d_into per image,
+// npu.rs:356).  One thread per output element, consecutive l per thread.
+__global__ __launch_bounds__(256) void nlo_to_nchw_kernel(const float* __restrict__ ylo, int64_t n, int64_t O,
+                                                          int64_t L, float* __restrict__ y) {
+  const int64_t total = n * O * L;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t img = e / (O * L);
+    const int64_t rem = e - img * O * L;
+    const int64_t o = rem / L, l = rem - o * L;
+    y[e] = ylo[(img * L + l) * O + o];
+  }
+}
+
+void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s) {
+  const int64_t total = n * O * L;
+  if (total <= 0) return;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(nlo_to_nchw_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ylo, n, O, L, y);
+}
+
+// Lone ChannelAffine in FP16: the diagonal FusedLinear's serial sum has a
+// single non-zero term, the product with the raw scale (npu.rs:254-270,
+// 433-445), so y = round_fp16(fl(round_fp16(x) * scale[c]) + shift[c]).
+__global__ __launch_bounds__(256) void affine_f16_kernel(const float* __restrict__ x, int64_t n, int64_t C,
+                                                         const float* __restrict__ scale,
+                                                         const float* __restrict__ shift, float* __restrict__ y) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c = e % C;
+    const float prod = rgmath::round_fp16(x[e]) * scale[c];
+    const float t = prod + shift[c];
+    y[e] = rgmath::round_fp16(t);
+  }
+}
+
+void launch_affine_f16(const float* x, int64_t n, int64_t C, const float* scale, const float* shift, float* y,
+                       hipStream_t s) {
+  if (n <= 0) return;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(affine_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, C, scale, shift, y);
+}
+
+// ---------------------------------------------------------------------------
 // quantize images (conv input): per-image scale, same element layout.
 // quantize(im2col(x)) == im2col(quantize(x)) elementwise, and padding zeros
 // quantize to 0, so the conv kernel gathers from the quantized image.
@@ -464,14 +609,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
-template <int ACT, bool CAP>
+template <int ACT, bool CAP, bool F16>
 __device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int rows, float* yp, int32_t* ap, int64_t N,
                                                       float cs, float b, float p, int lane) {
   uint32_t amax = 0;
 #pragma unroll 1
   for (int r = 0; r < rows; r++) {
     const int32_t a = slab[r * big::SLAB_LD + lane];
-    const float v = epi_value<ACT>(a, cs, b, p);
+    const float v = epi_word<ACT, F16>(a, cs, b, p);
     *yp = v;
     yp += N;
     if (CAP) {
@@ -488,7 +633,7 @@ __device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int r
 // time and stores it row-major: lane l owns column n0 + wn*64 + l, so each
 // store instruction writes 256 contiguous bytes.  The bias and scale were
 // loaded before the K loop.
-template <int ACT, bool CAP, int FM>
+template <int ACT, bool CAP, int FM, bool F16>
 __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                  int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                  int wave, int wm, int wn, int lane) {
@@ -508,24 +653,30 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
     const int rows = col_ok ? (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16) : 0;
     float* yp = ep.y + row0 * N + col;
     int32_t* ap = CAP ? ep.acc_out + row0 * N + col : nullptr;
-    const uint32_t a = big_epilogue_slab<ACT, CAP>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
+    const uint32_t a = big_epilogue_slab<ACT, CAP, F16>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
     amax = a > amax ? a : amax;
   }
   return amax;
 }
 
-template <int ACT, int FM>
+template <int ACT, int FM, bool F16>
 __device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                      int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                      int wave, int wm, int wn, int lane) {
-  return ep.acc_out ? big_epilogue<ACT, true, FM>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
-                    : big_epilogue<ACT, false, FM>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
+  return ep.acc_out ? big_epilogue<ACT, true, FM, F16>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
+                    : big_epilogue<ACT, false, FM, F16>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
 }
 
 // Split K: gridDim.y > 1 gives block (x, y) the K steps [y*ks, (y+1)*ks) and
-// it stores its raw i32 sums to ws[y][Mpad][Npad] for splitk_epilogue_kernel.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kernel(
+// it stores its raw sums to ws[y][Mpad][Npad] for splitk_epilogue_kernel.
+//
+// F16 (NpuPrecision::Fp16): A and B hold IEEE binary16 values, a K step of
+// 64 bytes is 32 of them and one v_mfma_f32_16x16x32_f16 per 16 x 16 block,
+// whose per-lane operand layout matches the i8 instruction's byte for byte,
+// so the DMA ring, swizzle and LDS reads are shared.  The f32 sums travel in
+// the same 32-bit accumulator words.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, bool F16>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int64_t M, int64_t N, int64_t Kpad, int tiles_m,
     int tiles_n, Epilogue ep, int ks, int32_t* __restrict__ ws) {
   using namespace big;
@@ -547,8 +698,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
   const int64_t my_col = n0 + wn * 64 + lane;
   const float bias_v = my_col < N ? ep.bias[my_col] : 0.0f;
   // Partial of the input absmax; folded after the K loop so the fold does not
-  // wait on the prologue DMA.
-  const uint32_t absmax_part = tensor_absmax_part(ep.absmax_in);
+  // wait on the prologue DMA.  (FP16 has no activation scale.)
+  uint32_t absmax_part = 0;
+  if constexpr (!F16) absmax_part = tensor_absmax_part(ep.absmax_in);
 
   // DMA addressing: uniform tile base pointers plus 32-bit per-lane offsets.
   // Wave w fills A rows [16 IA w, 16 IA (w+1)) and B rows [16 IB w, ...).
@@ -616,7 +768,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 4; j++) {
+        if constexpr (F16)
+          acc[i][j] = __builtin_bit_cast(
+              v4i, __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, af[i]), __builtin_bit_cast(v8h, bf[j]),
+                                                           __builtin_bit_cast(v4f, acc[i][j]), 0, 0, 0));
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
     st_rd = st_rd == (uint32_t)((STAGES - 1) * ST) ? 0 : st_rd + ST;
     st_is = st_is == (uint32_t)((STAGES - 1) * ST) ? 0 : st_is + ST;
   }
@@ -637,9 +796,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
     (void)absmax_part;
     return;
   }
-  const float cs = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
+  const float cs = F16 ? 1.0f : rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
   uint32_t amax = 0;
-#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV, FM>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
+#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV, FM, F16>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
   switch (ep.act) {
     case rgmath::ACT_RELU: amax = RG_BIG_EPI(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: amax = RG_BIG_EPI(rgmath::ACT_SIGMOID); break;
@@ -656,22 +815,31 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_i8_big_kerne
   }
 }
 
-// Split-K epilogue: y = act(float(sum of the S partial sums) * cs + bias).
-template <int ACT>
+// Split-K epilogue: the S partial sums added in slice order, then the fused
+// epilogue (INT8: exact i32 sum; FP16: f32 sum).
+template <int ACT, bool F16>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, int64_t Mpad, int64_t Npad, Epilogue ep) {
-  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  float cs = 1.0f;
+  if constexpr (!F16) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int64_t n4 = Npad / 4, total = M * n4;
   uint32_t amax = 0;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / n4, c0 = (e - row * n4) * 4;
     v4i sum = v4i{0, 0, 0, 0};
-    for (int sp = 0; sp < S; sp++) sum += *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0);
+    if constexpr (F16) {
+      v4f f = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int sp = 0; sp < S; sp++)
+        f += __builtin_bit_cast(v4f, *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0));
+      sum = __builtin_bit_cast(v4i, f);
+    } else {
+      for (int sp = 0; sp < S; sp++) sum += *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0);
+    }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int64_t col = c0 + q;
       if (col < N) {
-        const float v = epi_value<ACT>(sum[q], cs, ep.bias[col], ep.act_param);
+        const float v = epi_word<ACT, F16>(sum[q], cs, ep.bias[col], ep.act_param);
         ep.y[row * N + col] = v;
         if (ep.acc_out) ep.acc_out[row * N + col] = sum[q];
         const uint32_t k = rgmath::absmax_key(v);
@@ -685,13 +853,14 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __r
   }
 }
 
+template <bool F16>
 static void launch_splitk_epilogue(const int32_t* ws, int S, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                                    const Epilogue& ep, hipStream_t s) {
   int64_t blocks = (M * (Npad / 4) + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   if (blocks < 1) blocks = 1;
 #define RG_SKE(ACTV) \
-  RG_LAUNCH(splitk_epilogue_kernel<ACTV>, dim3((unsigned)blocks), dim3(256), 0, s, ws, S, M, N, Mpad, Npad, ep)
+  RG_LAUNCH((splitk_epilogue_kernel<ACTV, F16>), dim3((unsigned)blocks), dim3(256), 0, s, ws, S, M, N, Mpad, Npad, ep)
   switch (ep.act) {
     case rgmath::ACT_RELU: RG_SKE(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: RG_SKE(rgmath::ACT_SIGMOID); break;
@@ -704,13 +873,13 @@ static void launch_splitk_epilogue(const int32_t* ws, int S, int64_t M, int64_t 
 #undef RG_SKE
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, bool F16>
 static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                        int64_t Kpad, const Epilogue& ep, int splits, int32_t* ws, hipStream_t s) {
   const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
   const int nk = (int)(Kpad / big::BK);
   const int ks = (nk + splits - 1) / splits;
-  RG_LAUNCH((gemm_i8_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM>), dim3((unsigned)(tm * tn), (unsigned)splits),
+  RG_LAUNCH((gemm_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, F16>), dim3((unsigned)(tm * tn), (unsigned)splits),
             dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep, ks, ws);
 }
 
@@ -740,21 +909,33 @@ int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad) {
   return g.kind == 2 && g.splits > 1 ? (int64_t)g.splits * Mpad * Npad * 4 : 0;
 }
 
-void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
-                 const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
+template <bool F16>
+static void launch_gemm_t(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                          int64_t Kpad, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
   if (Kpad % big::BK || Mpad % 128 || Npad % 128 || Kpad <= 0)
     throw std::logic_error("GEMM operands must be padded to 128 rows and 64-byte K steps");
   const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
   if (g.kind == 0) {
-    launch_big<256, 256, 2, 4, 4, 1, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<256, 256, 2, 4, 4, 1, 8, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   } else if (g.kind == 1) {
-    launch_big<256, 128, 2, 2, 3, 2, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<256, 128, 2, 2, 3, 2, 8, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   } else if (g.splits > 1 && ws && ws_bytes >= (int64_t)g.splits * Mpad * Npad * 4) {
-    launch_big<128, 128, 2, 2, 4, 2, 4>(A, B, M, N, Mpad, Npad, Kpad, ep, g.splits, ws, s);
-    launch_splitk_epilogue(ws, g.splits, M, N, Mpad, Npad, ep, s);
+    launch_big<128, 128, 2, 2, 4, 2, 4, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, g.splits, ws, s);
+    launch_splitk_epilogue<F16>(ws, g.splits, M, N, Mpad, Npad, ep, s);
   } else {
-    launch_big<128, 128, 2, 2, 4, 2, 4>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<128, 128, 2, 2, 4, 2, 4, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   }
+}
+
+void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
+                 const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
+  launch_gemm_t<false>(A, B, M, N, Mpad, Npad, Kpad, ep, ws, ws_bytes, s);
+}
+
+void launch_gemm_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                     int64_t Kpad_h, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
+  launch_gemm_t<true>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Mpad, Npad,
+                      2 * Kpad_h, ep, ws, ws_bytes, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -96,11 +96,14 @@ struct Op {
   int64_t k = 0, s = 0, p = 0;  // Conv2d kernel/stride/pad, MaxPool2d kernel/stride
   int act = 0;
   float act_param = 0.0f;
-  std::vector<int8_t> wq;  // [out, K] as the reference holds it
+  std::vector<int8_t> wq;  // [out, K] as the reference holds it (INT8)
   float w_scale = 1.0f;
+  std::vector<float> wh;   // FP16: round_fp16 weights [out, K] (npu.rs:210, 232)
+  bool diag = false;       // FP16 lone ChannelAffine: elementwise, scale kept as is (npu.rs:254-270)
+  std::vector<float> diag_scale;
   std::vector<float> bias;
-  int64_t K = 0, Kpad = 0, Npad = 0;
-  DevBuf d_w, d_bias;
+  int64_t K = 0, Kpad = 0, Npad = 0;  // Kpad in bytes (INT8) or binary16 elements (FP16)
+  DevBuf d_w, d_bias, d_scale;
   std::string label;
 };
 
@@ -127,7 +130,7 @@ struct Plan {
   std::vector<int64_t> in_shape, out_shape;
   int64_t in_len = 0, out_len = 0;
   std::vector<OpPlan> ops;
-  size_t f32_elems = 0, q_bytes = 0;
+  size_t f32_elems = 0, q_bytes = 0, ylo_elems = 0;
   int64_t n_slots = 0;
   // Slot sets: with clear_by_first the slots are two sets of n_slots words;
   // run k uses set `parity` and its first kernel (the input absmax) zeroes
@@ -137,6 +140,7 @@ struct Plan {
   int parity = 0;
   int64_t slot_set_words = 0;  // n_slots rounded up to a 128-byte multiple
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
+  DevBuf ylo;  // FP16 conv: GEMM output [n*L, O] before the NCHW transpose
   DevBuf ws;  // split-K partial sums
   int64_t ws_bytes = 0;
   std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
@@ -153,6 +157,7 @@ using namespace rgnpu;
 
 struct rgnpu_program {
   int device = 0;
+  int precision = RGNPU_PRECISION_INT8;
   hipStream_t stream = nullptr;
   int64_t original_layers = 0;
   int64_t fp32_bytes = 0, npu_bytes = 0;
@@ -260,6 +265,27 @@ static float quantize_host(const float* v, int64_t n, int8_t* out) {
   return scale;
 }
 
+// FP16: binary16 [Npad, Kpad] from the rounded weights in the reference
+// order (Linear [out, in], Conv [out, c*k*k]), zero padded.
+static void upload_weights_f16(Op& op, hipStream_t s) {
+  std::vector<float> bpad((size_t)std::max<int64_t>(op.Npad, (int64_t)op.bias.size()), 0.0f);
+  std::memcpy(bpad.data(), op.bias.data(), sizeof(float) * op.bias.size());
+  op.d_bias.ensure(bpad.size() * sizeof(float));
+  RG_HIP(hipMemcpyAsync(op.d_bias.p, bpad.data(), bpad.size() * sizeof(float), hipMemcpyHostToDevice, s));
+  if (op.diag) {
+    op.d_scale.ensure(op.diag_scale.size() * sizeof(float));
+    RG_HIP(hipMemcpyAsync(op.d_scale.p, op.diag_scale.data(), op.diag_scale.size() * sizeof(float),
+                          hipMemcpyHostToDevice, s));
+  } else {
+    std::vector<uint16_t> h((size_t)(op.Npad * op.Kpad), 0);
+    for (int64_t r = 0; r < op.out_f; r++)
+      for (int64_t c = 0; c < op.K; c++) h[(size_t)(r * op.Kpad + c)] = rgmath::fp16_bits(op.wh[(size_t)(r * op.K + c)]);
+    op.d_w.ensure(h.size() * sizeof(uint16_t));
+    RG_HIP(hipMemcpyAsync(op.d_w.p, h.data(), h.size() * sizeof(uint16_t), hipMemcpyHostToDevice, s));
+  }
+  RG_HIP(hipStreamSynchronize(s));
+}
+
 static void upload_weights(Op& op, hipStream_t s) {
   // Linear: [N, K] host -> [Npad, Kpad] device, zero padded.  Conv: the
   // reference [O, C*k*k] order becomes tap-major [Opad, Kpad], kk' =
@@ -313,6 +339,7 @@ static std::string op_label(const Op& op) {
 
 // npu::compile (npu.rs:188-276).
 static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
+  const bool f16 = P->precision == RGNPU_PRECISION_FP16;
   for (int64_t i = 0; i < n; i++) check_layer(layers[i], i);
   P->original_layers = n;
   std::vector<FLayer> F = fold_batch_norm(layers, n);
@@ -335,13 +362,20 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
       std::vector<float> wt((size_t)(op->in_f * op->out_f));
       for (int64_t r = 0; r < op->in_f; r++)
         for (int64_t c = 0; c < op->out_f; c++) wt[(size_t)(c * op->in_f + r)] = f.w[(size_t)(r * op->out_f + c)];
-      op->wq.resize(wt.size());
-      op->w_scale = quantize_host(wt.data(), (int64_t)wt.size(), op->wq.data());
       op->bias = f.b;
       P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
-      P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
       op->Npad = round_up(op->out_f, kRowPad);
-      op->Kpad = round_up(op->K, kKPad);
+      if (f16) {
+        op->wh.resize(wt.size());
+        for (size_t j = 0; j < wt.size(); j++) op->wh[j] = rgmath::round_fp16(wt[j]);
+        P->npu_bytes += (int64_t)(f.w.size() + f.b.size()) * 2;
+        op->Kpad = round_up(op->K, kKPadHalf);
+      } else {
+        op->wq.resize(wt.size());
+        op->w_scale = quantize_host(wt.data(), (int64_t)wt.size(), op->wq.data());
+        P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
+        op->Kpad = round_up(op->K, kKPad);
+      }
     } else if (f.spec.kind == RGNPU_LAYER_CONV2D) {
       op->kind = OP_CONV;
       op->in_f = f.spec.in_channels;
@@ -350,13 +384,22 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
       op->s = f.spec.stride;
       op->p = f.spec.padding;
       op->K = op->in_f * op->k * op->k;
-      op->wq.resize(f.w.size());
-      op->w_scale = quantize_host(f.w.data(), (int64_t)f.w.size(), op->wq.data());  // [out, c*k*k] (npu.rs:231)
       op->bias = f.b;
       P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
-      P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
-      op->Npad = round_up(op->out_f, kConvOPad);
-      op->Kpad = conv_kpad(op->in_f, op->k);
+      if (f16) {
+        // the conv runs as im2col + GEMM: output channels are the GEMM's N
+        op->wh.resize(f.w.size());
+        for (size_t j = 0; j < f.w.size(); j++) op->wh[j] = rgmath::round_fp16(f.w[j]);
+        P->npu_bytes += (int64_t)(f.w.size() + f.b.size()) * 2;
+        op->Npad = round_up(op->out_f, kRowPad);
+        op->Kpad = round_up(op->K, kKPadHalf);
+      } else {
+        op->wq.resize(f.w.size());
+        op->w_scale = quantize_host(f.w.data(), (int64_t)f.w.size(), op->wq.data());  // [out, c*k*k] (npu.rs:231)
+        P->npu_bytes += ((int64_t)op->wq.size() + 4) + (int64_t)f.b.size() * 4;
+        op->Npad = round_up(op->out_f, kConvOPad);
+        op->Kpad = conv_kpad(op->in_f, op->k);
+      }
     } else if (f.spec.kind == RGNPU_LAYER_CHANNEL_AFFINE) {
       // Lone ChannelAffine -> diagonal Linear, no byte accounting (npu.rs:254-270).
       const int64_t c = (int64_t)f.scale.size();
@@ -365,11 +408,17 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
       op->kind = OP_LINEAR;
       op->in_f = op->out_f = op->K = c;
       op->act = rgmath::ACT_NONE;
-      op->wq.resize(w.size());
-      op->w_scale = quantize_host(w.data(), (int64_t)w.size(), op->wq.data());
       op->bias = f.shift;
       op->Npad = round_up(c, kRowPad);
-      op->Kpad = round_up(c, kKPad);
+      if (f16) {
+        op->diag = true;
+        op->diag_scale = f.scale;
+        op->Kpad = round_up(c, kKPadHalf);
+      } else {
+        op->wq.resize(w.size());
+        op->w_scale = quantize_host(w.data(), (int64_t)w.size(), op->wq.data());
+        op->Kpad = round_up(c, kKPad);
+      }
     } else if (f.spec.kind == RGNPU_LAYER_MAXPOOL2D) {
       op->kind = OP_POOL;
       op->k = f.spec.pool_kernel;
@@ -383,7 +432,12 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
     } else if (f.spec.kind == RGNPU_LAYER_SOFTMAX) {
       op->kind = OP_SOFTMAX;
     }
-    if (op->kind == OP_LINEAR || op->kind == OP_CONV) upload_weights(*op, P->stream);
+    if (op->kind == OP_LINEAR || op->kind == OP_CONV) {
+      if (f16)
+        upload_weights_f16(*op, P->stream);
+      else
+        upload_weights(*op, P->stream);
+    }
     op->label = op_label(*op);
     P->ops.push_back(std::move(op));
     i++;
@@ -437,7 +491,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
                                            " is not a multiple of in_features");
         pl.rows = pl.in_len / op.in_f;
         pl.macs = (uint64_t)(pl.rows * op.in_f * op.out_f);
-        pl.gemv = pl.rows <= 8;
+        pl.gemv = pl.rows <= 8 && P->precision == RGNPU_PRECISION_INT8;
         // the GEMV reads exactly `rows` activation rows; the MFMA GEMM reads
         // whole 256-row tiles
         pl.Mpad = pl.gemv ? (pl.rows > 0 ? pl.rows : 1) : round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
@@ -452,6 +506,8 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         const int64_t oh = out_size(h, op.k, op.s, op.p), ow = out_size(w, op.k, op.s, op.p);
         pl.cs = ConvShape{n, c, h, w, op.out_f, op.Npad, op.k, op.s, op.p, oh, ow, op.Kpad, conv_cp(c)};
         pl.macs = (uint64_t)(n * op.out_f * op.K * oh * ow);
+        pl.rows = n * oh * ow;  // FP16: GEMM rows of the im2col matrix
+        pl.Mpad = round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
         auto rm = coverage(h, op.k, op.s, op.p, oh), cm = coverage(w, op.k, op.s, op.p, ow);
         pl.full_cov = true;
         for (auto v : rm) pl.full_cov &= v != 0;
@@ -511,6 +567,15 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR && op.kind != OP_CONV) continue;
+    if (P->precision == RGNPU_PRECISION_FP16) {
+      // No activation quantization: binary16 operands, the split-K
+      // workspace, and the conv's [n*L, O] GEMM output.
+      if (op.diag) continue;
+      plan->q_bytes = std::max(plan->q_bytes, (size_t)(pl.Mpad * op.Kpad) * 2);
+      plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, 2 * op.Kpad));
+      if (op.kind == OP_CONV) plan->ylo_elems = std::max(plan->ylo_elems, (size_t)(pl.rows * op.out_f));
+      continue;
+    }
     pl.slot_count = op.kind == OP_LINEAR ? 1 : pl.cs.n;
     if (op.kind == OP_LINEAR) {
       pl.slot_base = round_up(slots, kSpreadStride);
@@ -557,6 +622,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   plan->f32[0].ensure(plan->f32_elems * sizeof(float));
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
   plan->q.ensure(plan->q_bytes);
+  if (plan->ylo_elems > 0) plan->ylo.ensure(plan->ylo_elems * sizeof(float));
   if (plan->ws_bytes > 0) plan->ws.ensure((size_t)plan->ws_bytes);
   plan->slot_set_words = round_up(std::max<int64_t>(slots, 1), kSpreadStride);
   const size_t slot_bytes = (size_t)plan->slot_set_words * sizeof(uint32_t) * (plan->clear_by_first ? 2 : 1);
@@ -581,7 +647,7 @@ static void ensure_capture_buffers(rgnpu_program* P, Plan& plan) {
     const OpPlan& pl = plan.ops[i];
     plan.cap_out[i] = std::make_unique<DevBuf>();
     plan.cap_out[i]->ensure((size_t)pl.out_len * sizeof(float));
-    if (op.kind == OP_LINEAR || op.kind == OP_CONV) {
+    if ((op.kind == OP_LINEAR || op.kind == OP_CONV) && P->precision == RGNPU_PRECISION_INT8) {
       plan.cap_q[i] = std::make_unique<DevBuf>();
       plan.cap_acc[i] = std::make_unique<DevBuf>();
       plan.cap_q[i]->ensure(op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len);
@@ -645,6 +711,7 @@ static void op_times(const rgnpu_program* P, const Plan& plan, const hipEvent_t*
 // bound each op.  A null `ev` records nothing (back-to-back throughput runs).
 static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipEvent_t* ev, bool timed) {
   hipStream_t s = P->stream;
+  const bool f16 = P->precision == RGNPU_PRECISION_FP16;
   const bool cap = P->capture;
   struct SinkOff {
     ~SinkOff() { set_launch_events(nullptr, 0); }
@@ -688,6 +755,24 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     uint32_t* emit = pl.emit_slot >= 0 ? slots + pl.emit_slot : nullptr;
     switch (op.kind) {
       case OP_LINEAR: {
+        if (f16) {  // npu.rs:315
+          pre = launch_events_used();
+          if (op.diag) {
+            launch_affine_f16(in, pl.in_len, op.in_f, op.d_scale.as<float>(), op.d_bias.as<float>(), out, s);
+          } else if (pl.rows > 0) {
+            uint16_t* h = plan.q.as<uint16_t>();
+            launch_half_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, h, s);
+            Epilogue ep;
+            ep.bias = op.d_bias.as<float>();
+            ep.act = op.act;
+            ep.act_param = op.act_param;
+            ep.y = out;
+            pre = launch_events_used();
+            launch_gemm_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                            plan.ws.as<int32_t>(), plan.ws_bytes, s);
+          }
+          break;
+        }
         uint32_t* slot = slots + pl.slot_base;
         if (pl.explicit_absmax) {
           launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s, clear);
@@ -717,6 +802,23 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
       }
       case OP_CONV: {
         const ConvShape& c = pl.cs;
+        if (f16) {  // npu.rs:341-376: im2col, GEMM, transpose per image
+          pre = launch_events_used();
+          if (pl.rows > 0) {
+            uint16_t* h = plan.q.as<uint16_t>();
+            launch_im2col_half(in, c, pl.Mpad, op.Kpad, h, s);
+            Epilogue ep;
+            ep.bias = op.d_bias.as<float>();
+            ep.act = op.act;
+            ep.act_param = op.act_param;
+            ep.y = plan.ylo.as<float>();
+            pre = launch_events_used();
+            launch_gemm_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                            plan.ws.as<int32_t>(), plan.ws_bytes, s);
+            launch_nlo_to_nchw(plan.ylo.as<float>(), c.n, op.out_f, c.OH * c.OW, out, s);
+          }
+          break;
+        }
         uint32_t* sl = slots + pl.slot_base;
         const int64_t per = c.C * c.H * c.W;
         if (pl.explicit_absmax) {
@@ -791,7 +893,7 @@ static void finalize_profile(rgnpu_program* P) {
   RG_HIP(hipEventSynchronize(P->ev[1]));
   Plan& plan = *P->plan;
   rgnpu_profile pr{};
-  pr.precision = RGNPU_PRECISION_INT8;
+  pr.precision = P->precision;
   pr.original_layers = (int32_t)P->original_layers;
   pr.fused_ops = (int32_t)P->ops.size();
   pr.fp32_weight_bytes = (uint64_t)P->fp32_bytes;
@@ -856,14 +958,14 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
   if (!out) throw Error(RGNPU_ERR_INVALID, "out is NULL");
   *out = nullptr;
   if (n_layers < 0 || (n_layers > 0 && !layers)) throw Error(RGNPU_ERR_INVALID, "invalid layer list");
-  if (precision == RGNPU_PRECISION_FP16)
-    throw Error(RGNPU_ERR_UNSUPPORTED, "NpuPrecision::Fp16 is not provided by the MI355X provider");
-  if (precision != RGNPU_PRECISION_INT8) throw Error(RGNPU_ERR_INVALID, "unknown precision");
+  if (precision != RGNPU_PRECISION_INT8 && precision != RGNPU_PRECISION_FP16)
+    throw Error(RGNPU_ERR_INVALID, "unknown precision");
   int count = 0;
   RG_HIP(hipGetDeviceCount(&count));
   if (device < 0 || device >= count) throw Error(RGNPU_ERR_DEVICE, "device index out of range");
   auto P = std::make_unique<rgnpu_program>();
   P->device = device;
+  P->precision = precision;
   RG_HIP(hipSetDevice(device));
   RG_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
   try {
@@ -1044,9 +1146,9 @@ int64_t rgnpu_program_summary(const rgnpu_program* P, char* buf, int64_t cap) {
   }
   char head[512];
   snprintf(head, sizeof head,
-           "InferenceSession [provider = MI355X (INT8), layers: %lld -> %zu fused ops, weights: %lld B -> %lld B (%.2fx "
+           "InferenceSession [provider = MI355X (%s), layers: %lld -> %zu fused ops, weights: %lld B -> %lld B (%.2fx "
            "compression)]\n  Pipeline: ",
-           (long long)P->original_layers, P->ops.size(), (long long)P->fp32_bytes, (long long)P->npu_bytes, (double)ratio);
+           P->precision == RGNPU_PRECISION_FP16 ? "FP16" : "INT8", (long long)P->original_layers, P->ops.size(), (long long)P->fp32_bytes, (long long)P->npu_bytes, (double)ratio);
   std::string s = std::string(head) + names;
   if (buf && cap > 0) snprintf(buf, (size_t)cap, "%s", s.c_str());
   return (int64_t)s.size();
@@ -1073,7 +1175,8 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
     Plan& plan = *P->plan;
     const Op& op = *P->ops[(size_t)i];
     const OpPlan& pl = plan.ops[(size_t)i];
-    const bool gemm = op.kind == OP_LINEAR || op.kind == OP_CONV;
+    // FP16 has no quantized activations, scales or integer sums to expose.
+    const bool gemm = (op.kind == OP_LINEAR || op.kind == OP_CONV) && P->precision == RGNPU_PRECISION_INT8;
     auto copy_out = [&](const void* src, int64_t count, size_t elem) -> int64_t {
       if (dst) {
         const int64_t bytes = std::min<int64_t>(cap_bytes, count * (int64_t)elem);

@@ -10,6 +10,7 @@ namespace rgnpu {
 // zero rows/columns so every MFMA tile load stays in bounds.
 constexpr int64_t kRowPad = 256;   // Linear output features and activation rows
 constexpr int64_t kKPad = 128;     // reduction dimension (bytes)
+constexpr int64_t kKPadHalf = 32;  // FP16 reduction dimension (binary16 elements: one 64-byte K step)
 constexpr int64_t kConvOPad = 32;  // conv output channels
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
@@ -103,6 +104,25 @@ inline int64_t conv_cp(int64_t C) { return C <= 4 ? 4 : round_up(C, 16); }
 inline int64_t conv_kpad(int64_t C, int64_t k) { return round_up(k * k * conv_cp(C), 64); }
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
                  hipStream_t s);
+
+// ---- NpuPrecision::Fp16 ----------------------------------------------------
+// GEMM on IEEE binary16 operands (A [Mpad, Kpad_h], B [Npad, Kpad_h], Kpad_h a
+// multiple of 32), f32 accumulation, epilogue y = act(round_fp16(acc + bias))
+// (npu.rs:433-445).  Same tile choice and split-K workspace as launch_gemm
+// with Kpad = 2 * Kpad_h bytes.
+void launch_gemm_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                     int64_t Kpad_h, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s);
+// x f32 [M, K] -> binary16 round_fp16(x) [Mpad, Kpad_h], zero padded.
+void launch_half_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_h, uint16_t* h,
+                      hipStream_t s);
+// im2col of an NCHW batch in binary16: [Mpad >= n*L, Kpad_h >= C*k*k], reference column order.
+void launch_im2col_half(const float* x, const ConvShape& cs, int64_t Mpad, int64_t Kpad_h, uint16_t* h,
+                        hipStream_t s);
+// [n*L, O] -> NCHW [n, O, L].
+void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s);
+// Lone ChannelAffine: y = round_fp16(fl(round_fp16(x) * scale[c]) + shift[c]), c = index % C.
+void launch_affine_f16(const float* x, int64_t n, int64_t C, const float* scale, const float* shift, float* y,
+                       hipStream_t s);
 
 // Max pool (kernels.rs:165-213 semantics) with optional absmax of the output.
 void launch_maxpool(const float* x, float* y, int64_t n, int64_t C, int64_t H, int64_t W,

@@ -232,6 +232,10 @@ class ExecutionProvider:
         return ExecutionProvider("mi355x", NpuPrecision.Int8, device)
 
     @staticmethod
+    def mi355x_fp16(device: int = 0) -> "ExecutionProvider":
+        return ExecutionProvider("mi355x", NpuPrecision.Fp16, device)
+
+    @staticmethod
     def Npu(precision: NpuPrecision) -> "ExecutionProvider":
         return ExecutionProvider("npu", precision)
 
