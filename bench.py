@@ -31,7 +31,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "INT8 InferenceSession samples/s; achieved TOPS as % of i8 MFMA peak"
+METRIC_FP16 = "FP16 InferenceSession samples/s; achieved TFLOP/s as % of f16 MFMA peak"
 PEAK_I8_TOPS = 5000.0     # MI355X dense i8 MFMA, 5.0 POP/s
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
 
 
@@ -87,25 +89,27 @@ def measured_traffic(workload: str, kernel: str):
     return None
 
 
-def dominant_roofline(name, records, layers, x, workload):
+def dominant_roofline(name, records, layers, x, workload, fp16=False):
     """Roofline of the dominant kernel (largest total kernel time per step)."""
+    peak = PEAK_F16_TFLOPS if fp16 else PEAK_I8_TOPS
+    eb = 2 if fp16 else 1  # bytes per weight / activation element
     best = max(range(len(records)), key=lambda i: records[i].kernel_ns)
     r = records[best]
     if r.kernel_ns <= 0:
         return None, best
     secs = r.kernel_ns / 1e9
     if name == "gemv":
-        # algorithmic bytes of one GEMV launch: i8 weights N*K + f32 bias N +
-        # i8 activations B*K + f32 output B*N (the weight stream dominates)
+        # algorithmic bytes of one GEMV launch: weights N*K + f32 bias N +
+        # activations B*K (i8, or binary16 for FP16) + f32 output B*N
         lin = [l for l in layers if type(l).__name__ == "Linear"]
         idx = [i for i, rr in enumerate(records) if "Gemm" in rr.op][: len(lin)]
         li = lin[idx.index(best)] if best in idx else lin[0]
         b = x.shape[0]
-        byts = li.in_features * li.out_features + 4 * li.out_features + b * li.in_features + 4 * b * li.out_features
+        byts = eb * li.in_features * li.out_features + 4 * li.out_features + eb * b * li.in_features + 4 * b * li.out_features
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
-                "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None if fp16 else measured_traffic(workload, r.op),
+                "kernel": r.op, "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     if r.macs == 0:
         # elementwise op (copy calibration): f32 in + f32 out
         byts = 8 * int(np.prod(x.shape))
@@ -115,19 +119,20 @@ def dominant_roofline(name, records, layers, x, workload):
                 "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     ops = 2 * r.macs
     ach = ops / secs / 1e12
-    return {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
-            "frac": round(ach / PEAK_I8_TOPS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
+    return {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(ach / peak, 4), "traffic": None if fp16 else measured_traffic(workload, r.op), "kernel": r.op,
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 
-def cpu_baseline(name, layers, x, target_s: float):
-    """The oracle (C restatement of the reference's rayon INT8 path) on a
-    bounded sample of the same workload, all host threads: a probe pass over
-    a row sample, then as many passes as fill about target_s seconds."""
+def cpu_baseline(name, layers, x, target_s: float, fp16=False):
+    """The oracle (C restatement of the reference's rayon INT8 path, or of
+    its FP16 path) on a bounded sample of the same workload, all host
+    threads: a probe pass over a row sample, then as many passes as fill
+    about target_s seconds."""
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     oracle.set_threads(threads)
-    prog = oracle.RefProgram(layers)
+    prog = oracle.RefProgram(layers, precision=oracle.FP16 if fp16 else oracle.INT8)
     n = x.shape[0]
     rows = n if name in ("gemv", "copy") else max(1, min(n, 64))
     t0 = time.perf_counter()
@@ -144,6 +149,13 @@ def cpu_baseline(name, layers, x, target_s: float):
         prog.run(x[:rows], parallel=True)
     dt = time.perf_counter() - t0
     eff = min(rows, threads)
+    if fp16:
+        # the reference's FP16 Linear is serial (npu.rs:433-445); only conv
+        # images run in parallel (npu.rs:331)
+        cores = threads if name == "cnn" else 1
+        return {"value": round(passes * rows / dt, 3), "unit": "samples/s", "cores": cores, "kind": "port",
+                "sample": f"{passes} pass(es) over {rows} of {n} samples of the same workload ({dt:.1f} s); FP16 "
+                          f"path: Linear serial as in the reference, conv image-parallel"}
     return {"value": round(passes * rows / dt, 3), "unit": "samples/s", "cores": threads, "kind": "port",
             "sample": f"{passes} pass(es) over {rows} of {n} samples of the same workload ({dt:.1f} s); row-parallel "
                       f"like rayon (quantize.rs:104), effective parallelism min(rows, threads) = {eff}"}
@@ -161,6 +173,8 @@ def main():
                     help="activation of the linear_stack workload (gelu is the benchmark config)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--precision", default="int8", choices=["int8", "fp16"],
+                    help="NpuPrecision of the session (the headline metric is INT8)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (sharding is described in "
@@ -171,7 +185,9 @@ def main():
 
     t_setup = time.perf_counter()
     layers, x, config = build_workload(args.workload, args.batch, args.stack_act)
-    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    fp16 = args.precision == "fp16"
+    provider = rg.ExecutionProvider.mi355x_fp16() if fp16 else rg.ExecutionProvider.mi355x_int8()
+    sess = rg.InferenceSession.from_layers(layers, provider)
     out_shape = sess.output_shape(x.shape)
     dx = rg.DeviceBuffer.from_array(x)
     dy = rg.DeviceBuffer(int(np.prod(out_shape)) * 4)
@@ -197,17 +213,19 @@ def main():
     value = batch / (ms_per_step / 1e3)
     total_macs = sum(r.macs for r in recs)
     tops = 2 * total_macs / (ms_per_step / 1e3) / 1e12
-    roof, dom = dominant_roofline(args.workload, recs, layers, x, config["workload"])
+    roof, dom = dominant_roofline(args.workload, recs, layers, x, config["workload"], fp16)
     for r in recs:
         print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.duration_ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
               file=sys.stderr)
     line = {
-        "metric": METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "i8",
+        "metric": METRIC_FP16 if fp16 else METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16" if fp16 else "i8",
         "data": "synthetic: RustGears SplitMix64 seeded weights and inputs (rustgears_amd/configs.py)",
         "config": config,
-        "tops": round(tops, 2), "tops_frac_of_i8_peak": round(tops / PEAK_I8_TOPS, 4),
+        "tops": round(tops, 2),
+        ("tflops_frac_of_f16_peak" if fp16 else "tops_frac_of_i8_peak"):
+            round(tops / (PEAK_F16_TFLOPS if fp16 else PEAK_I8_TOPS), 4),
         "ms_per_step_with_kernel_events": round(dev_ms_ev / args.steps, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": roof,
@@ -223,7 +241,7 @@ def main():
     line["pcie_inclusive"] = {"value": round(batch / host_s, 2), "unit": "samples/s", "ms_per_step": round(host_s * 1e3, 3),
                               "steps": n_host, "note": "host-pointer run(): H2D input + run + D2H output, wall clock"}
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, fp16)
     print(json.dumps(line), flush=True)
 
 

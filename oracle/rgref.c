@@ -609,7 +609,8 @@ int rgref_execute(rgref_program* P, const float* x, const int64_t* shape_in, int
       op->macs = rows * in * out;
       if (P->precision == RGREF_FP16) {                                /* npu.rs:315 */
         float* y = (float*)xmalloc(sizeof(float) * (size_t)(rows * out));
-        rgref_fp16_gemm_fused(data, op->wh, rows, in, out, op->bias, op->act, op->act_param, y, parallel);
+        /* serial, as the reference runs it (no rayon split for FP16 Linear) */
+        rgref_fp16_gemm_fused(data, op->wh, rows, in, out, op->bias, op->act, op->act_param, y, 0);
         free(data); data = y; len = rows * out;
         shape[nd - 1] = out;
         goto op_done;

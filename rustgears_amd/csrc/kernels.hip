@@ -21,6 +21,7 @@ namespace rgnpu {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // Launch-event sink (see set_launch_events): every kernel launched while it
 // is set carries the next event as the stop event of its own dispatch.
@@ -968,34 +969,43 @@ __device__ __forceinline__ int32_t dpp_partner(int32_t v) {
   return __builtin_amdgcn_update_dpp(0, v, ctrl, 0xf, 0xf, false);
 }
 
+// Sum of two 32-bit words: i32 (INT8 sums) or the f32 values they hold (FP16).
+template <bool F>
+__device__ __forceinline__ int32_t add_word(int32_t a, int32_t b) {
+  if constexpr (F)
+    return __float_as_int(__int_as_float(a) + __int_as_float(b));
+  else
+    return a + b;
+}
+
 // Lanes with bit OFF clear get lo + partner's lo, the others hi + partner's hi.
-template <int OFF>
+template <int OFF, bool F = false>
 __device__ __forceinline__ int32_t pair_combine(int32_t lo, int32_t hi, int lane) {
   if constexpr (OFF == 32) {
     const auto p = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
-    return (int32_t)(p[0] + p[1]);
+    return add_word<F>((int32_t)p[0], (int32_t)p[1]);
   } else if constexpr (OFF == 16) {
     const auto p = __builtin_amdgcn_permlane16_swap(lo, hi, false, false);
-    return (int32_t)(p[0] + p[1]);
+    return add_word<F>((int32_t)p[0], (int32_t)p[1]);
   } else {
     const bool up = (lane & OFF) != 0;
-    return (up ? hi : lo) + dpp_partner<OFF>(up ? lo : hi);
+    return add_word<F>(up ? hi : lo, dpp_partner<OFF>(up ? lo : hi));
   }
 }
 
-template <int OFF>
-__device__ __forceinline__ int32_t fold(int32_t t, int lane) { return pair_combine<OFF>(t, t, lane); }
+template <int OFF, bool F = false>
+__device__ __forceinline__ int32_t fold(int32_t t, int lane) { return pair_combine<OFF, F>(t, t, lane); }
 
 // Reduce-scatter butterfly over the wave: S partial sums per lane in, one
 // finished sum out; lane l holds sum l / (64 / S).  S - 1 exchanges while
 // the sums halve, then log2(64 / S) folds of the last one.
-template <int S>
+template <int S, bool F = false>
 __device__ __forceinline__ int32_t wave_reduce_scatter(int32_t (&v)[S], int lane) {
   static_assert(S >= 1 && S <= 64 && (S & (S - 1)) == 0, "S must be a power of two <= 64");
 #define RG_RS_STEP(OFF, DIV)                                                  \
   if constexpr (S >= DIV) {                                                   \
     _Pragma("unroll") for (int i = 0; i < S / DIV; i++)                       \
-      v[i] = pair_combine<OFF>(v[i], v[i + S / DIV], lane);                   \
+      v[i] = pair_combine<OFF, F>(v[i], v[i + S / DIV], lane);                \
   }
   RG_RS_STEP(32, 2)
   RG_RS_STEP(16, 4)
@@ -1005,25 +1015,30 @@ __device__ __forceinline__ int32_t wave_reduce_scatter(int32_t (&v)[S], int lane
   RG_RS_STEP(1, 64)
 #undef RG_RS_STEP
   int32_t t = v[0];
-  if constexpr (S < 2) t = fold<32>(t, lane);
-  if constexpr (S < 4) t = fold<16>(t, lane);
-  if constexpr (S < 8) t = fold<8>(t, lane);
-  if constexpr (S < 16) t = fold<4>(t, lane);
-  if constexpr (S < 32) t = fold<2>(t, lane);
-  if constexpr (S < 64) t = fold<1>(t, lane);
+  if constexpr (S < 2) t = fold<32, F>(t, lane);
+  if constexpr (S < 4) t = fold<16, F>(t, lane);
+  if constexpr (S < 8) t = fold<8, F>(t, lane);
+  if constexpr (S < 16) t = fold<4, F>(t, lane);
+  if constexpr (S < 32) t = fold<2, F>(t, lane);
+  if constexpr (S < 64) t = fold<1, F>(t, lane);
   return t;
 }
 
 constexpr int pow2_at_least(int v) { return v <= 1 ? 1 : 2 * pow2_at_least((v + 1) / 2); }
 
-template <int MR, int R, int U>
-__global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                      int64_t N, int64_t groups, int64_t Kpad, Epilogue ep) {
+// F16 (NpuPrecision::Fp16): A and B hold binary16 values (8 per 16-byte
+// chunk), the partial sums are f32 from v_dot2_f32_f16 (exact products; the
+// summation order differs from the reference's serial one), and the
+// epilogue is act(round_fp16(acc + bias)).
+template <int MR, int R, int U, bool F16>
+__global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                   int64_t N, int64_t groups, int64_t Kpad, Epilogue ep) {
   constexpr int S = pow2_at_least(MR * R);
   constexpr int SPREAD = 64 / S;  // lanes holding the same finished sum
   const int lane = threadIdx.x & 63;
   const int64_t waves = (int64_t)gridDim.x * 4;
-  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  float cs = 1.0f;
+  if constexpr (!F16) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int sidx = lane / SPREAD;
   const int om = sidx / R, orr = sidx % R;
   const bool owner = (lane % SPREAD) == 0 && sidx < MR * R;
@@ -1066,18 +1081,33 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__
 #pragma unroll
           for (int r = 0; r < R; r++) {
             int32_t a = acc[m * R + r];
-            a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
-            a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
-            a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
-            a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+            if constexpr (F16) {
+              const v8h xh = __builtin_bit_cast(v8h, xv), wh = __builtin_bit_cast(v8h, w[u][r]);
+              float f = __int_as_float(a);
+#pragma unroll
+              for (int q = 0; q < 4; q++)
+                f = __builtin_amdgcn_fdot2(v2h{xh[2 * q], xh[2 * q + 1]}, v2h{wh[2 * q], wh[2 * q + 1]}, f, false);
+              a = __float_as_int(f);
+            } else {
+              a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
+              a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
+              a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
+              a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+            }
             acc[m * R + r] = a;
           }
         }
     }
-    const int32_t mine = wave_reduce_scatter<S>(acc, lane);
-    // (acc as f32) * cs + bias with separate roundings, as in epi_value.
-    const float prod = (float)mine * cs;
-    const float pre = prod + bias_v;
+    const int32_t mine = wave_reduce_scatter<S, F16>(acc, lane);
+    // INT8: (acc as f32) * cs + bias with separate roundings, as in
+    // epi_value.  FP16: round_fp16(acc + bias).
+    float pre;
+    if constexpr (F16) {
+      pre = rgmath::round_fp16(__int_as_float(mine) + bias_v);
+    } else {
+      const float prod = (float)mine * cs;
+      pre = prod + bias_v;
+    }
     if (owner && col < N) {
       float v;
       switch (ep.act) {
@@ -1102,42 +1132,54 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(const int8_t* __restrict__
 }
 
 
-template <int MR, int R, int U>
+template <int MR, int R, int U, bool F16>
 void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, int64_t Kpad, const Epilogue& ep,
                    hipStream_t s, int64_t max_blocks) {
-  const void* fn = reinterpret_cast<const void*>(&gemv_i8_kernel<MR, R, U>);
+  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, R, U, F16>);
   static const int64_t cap = resident_blocks(fn);
   const int64_t groups = Npad / R;  // Npad is a multiple of 256, so of every R used
   int64_t blocks = (groups + 3) / 4;
   const int64_t lim = max_blocks > 0 ? max_blocks : cap;
   if (blocks > lim) blocks = lim;
-  RG_LAUNCH((gemv_i8_kernel<MR, R, U>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
+  RG_LAUNCH((gemv_kernel<MR, R, U, F16>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
 }
 
-void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
-                 const Epilogue& ep, hipStream_t s) {
+template <bool F16>
+static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
+                            const Epilogue& ep, hipStream_t s) {
   // (R, U) from a sweep on the decode shapes (8192 x 28672 and 28672 x
   // 8192): more rows share each activation load as M grows; long K rows
   // favour 8 rows per wave.
   const bool long_k = Kpad >= 16384;
   switch (M) {
-    case 1: launch_gemv_t<1, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 2: launch_gemv_t<2, 4, 4>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 3: launch_gemv_t<3, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 4: launch_gemv_t<4, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 1: launch_gemv_t<1, 4, 4, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 2: launch_gemv_t<2, 4, 4, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 3: launch_gemv_t<3, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 4: launch_gemv_t<4, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
     case 5:
-      long_k ? launch_gemv_t<5, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<5, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<5, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<5, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     case 6:
-      long_k ? launch_gemv_t<6, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<6, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<6, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<6, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     case 7:
-      long_k ? launch_gemv_t<7, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<7, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<7, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<7, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     default:
-      long_k ? launch_gemv_t<8, 8, 1>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<8, 4, 1>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<8, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<8, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
   }
+}
+
+void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
+                 const Epilogue& ep, hipStream_t s) {
+  launch_gemv_any<false>(A, B, M, N, Npad, Kpad, ep, s);
+}
+
+void launch_gemv_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_h,
+                     const Epilogue& ep, hipStream_t s) {
+  launch_gemv_any<true>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Npad, 2 * Kpad_h,
+                        ep, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -391,7 +391,7 @@ static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
         op->wh.resize(f.w.size());
         for (size_t j = 0; j < f.w.size(); j++) op->wh[j] = rgmath::round_fp16(f.w[j]);
         P->npu_bytes += (int64_t)(f.w.size() + f.b.size()) * 2;
-        op->Npad = round_up(op->out_f, kRowPad);
+        op->Npad = round_up(op->out_f, 128);  // the GEMM's smallest N tile
         op->Kpad = round_up(op->K, kKPadHalf);
       } else {
         op->wq.resize(f.w.size());
@@ -491,7 +491,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
                                            " is not a multiple of in_features");
         pl.rows = pl.in_len / op.in_f;
         pl.macs = (uint64_t)(pl.rows * op.in_f * op.out_f);
-        pl.gemv = pl.rows <= 8 && P->precision == RGNPU_PRECISION_INT8;
+        pl.gemv = pl.rows <= 8;
         // the GEMV reads exactly `rows` activation rows; the MFMA GEMM reads
         // whole 256-row tiles
         pl.Mpad = pl.gemv ? (pl.rows > 0 ? pl.rows : 1) : round_up(pl.rows > 0 ? pl.rows : 1, kRowPad);
@@ -572,7 +572,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
       // workspace, and the conv's [n*L, O] GEMM output.
       if (op.diag) continue;
       plan->q_bytes = std::max(plan->q_bytes, (size_t)(pl.Mpad * op.Kpad) * 2);
-      plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, 2 * op.Kpad));
+      if (!pl.gemv) plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, 2 * op.Kpad));
       if (op.kind == OP_CONV) plan->ylo_elems = std::max(plan->ylo_elems, (size_t)(pl.rows * op.out_f));
       continue;
     }
@@ -768,8 +768,11 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             ep.act_param = op.act_param;
             ep.y = out;
             pre = launch_events_used();
-            launch_gemm_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
-                            plan.ws.as<int32_t>(), plan.ws_bytes, s);
+            if (pl.gemv)
+              launch_gemv_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+            else
+              launch_gemm_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                              plan.ws.as<int32_t>(), plan.ws_bytes, s);
           }
           break;
         }

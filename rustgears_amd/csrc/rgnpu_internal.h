@@ -112,6 +112,9 @@ void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const 
 // with Kpad = 2 * Kpad_h bytes.
 void launch_gemm_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                      int64_t Kpad_h, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s);
+// GEMV for M <= 8 on binary16 operands (A [M, Kpad_h]), same epilogue.
+void launch_gemv_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_h,
+                     const Epilogue& ep, hipStream_t s);
 // x f32 [M, K] -> binary16 round_fp16(x) [Mpad, Kpad_h], zero padded.
 void launch_half_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_h, uint16_t* h,
                       hipStream_t s);

@@ -199,3 +199,12 @@ def test_fp16_report_and_accounting(rg, ref):
     assert "(FP16)" in rep and f"{p.fp32_bytes} B -> {p.npu_bytes} B" in rep, rep
     assert p.npu_bytes == (16 * 64 + 64 + 64 * 4 + 4) * 2
     sess.close()
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_fp16_gemv_decode_shape(rg, ref, batch):
+    """The decode-shape config (SiLU then a plain Linear) scaled down, through
+    the binary16 GEMV (batch <= 8)."""
+    from rustgears_amd import configs
+    layers, x = configs.gemv(batch=batch, d=1024, h=3584)
+    check_per_op(rg, ref, layers, x, f"gemv fp16 b{batch}")
