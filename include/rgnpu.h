@@ -93,10 +93,15 @@ typedef struct rgnpu_profile {
 } rgnpu_profile;
 
 /* Compile a layer list (fold_batch_norm, Linear/Conv2d+Activation fusion,
- * per-tensor i8 weight quantization) and upload the weights to `device`.
- * Replaces npu::compile (src/inference/npu.rs:188-276) as called from
- * InferenceSession::from_layers (src/inference/mod.rs:172).  Only
- * RGNPU_PRECISION_INT8 is provided; FP16 returns RGNPU_ERR_UNSUPPORTED. */
+ * per-tensor i8 weight quantization, or round_fp16 weights for
+ * RGNPU_PRECISION_FP16) and upload the weights to `device`.  Replaces
+ * npu::compile (src/inference/npu.rs:188-276) as called from
+ * InferenceSession::from_layers (src/inference/mod.rs:172).  INT8 results
+ * are bit-exact with the reference; FP16 sums in a different order than the
+ * reference's serial f32 loop (npu.rs:433-445), so its results agree within
+ * that reordering (see the test suite's bound), and an activation or weight
+ * whose round_fp16 value is +-65536 (inputs in [65520, 65536)) saturates to
+ * +-65504, the largest binary16 value. */
 int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t precision,
                          int32_t device, rgnpu_program** out);
 
