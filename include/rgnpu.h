@@ -50,8 +50,11 @@ enum {
   RGNPU_ACT_NONE = 0, RGNPU_ACT_RELU = 1, RGNPU_ACT_SIGMOID = 2, RGNPU_ACT_TANH = 3,
   RGNPU_ACT_GELU = 4, RGNPU_ACT_LEAKY_RELU = 5, RGNPU_ACT_SILU = 6
 };
-/* NpuPrecision (src/inference/npu.rs:25-30). */
-enum { RGNPU_PRECISION_INT8 = 0, RGNPU_PRECISION_FP16 = 1 };
+/* NpuPrecision (src/inference/npu.rs:25-30), plus RGNPU_PRECISION_FP32: the
+ * standard FP32 path of ExecutionProvider::Cpu / Gpu(i) (run_standard,
+ * src/inference/mod.rs:260-331) on the MI355X, replacing the wgpu matmul
+ * (src/device/gpu/wgpu_impl.rs:7-50). */
+enum { RGNPU_PRECISION_INT8 = 0, RGNPU_PRECISION_FP16 = 1, RGNPU_PRECISION_FP32 = 2 };
 
 /* One LayerSpec.  Weight layouts are exactly as Module::export produces
  * them: Linear weight [in_features, out_features] row-major

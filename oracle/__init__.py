@@ -84,6 +84,7 @@ def lib() -> ctypes.CDLL:
             ("rgref_compile", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64]),
             ("rgref_compile_precision", ctypes.c_void_p, [ctypes.POINTER(RefLayer), ctypes.c_int64, ctypes.c_int]),
             ("rgref_round_fp16", ctypes.c_float, [ctypes.c_float]),
+            ("rgref_matmul_f32", None, [f32p, f32p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, f32p, ctypes.c_int]),
             ("rgref_round_fp16_array", None, [f32p, f32p, ctypes.c_int64]),
             ("rgref_program_op_weight_fp16", ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int64, ctypes.POINTER(f32p),
                                                               i64p]),
@@ -230,7 +231,7 @@ def to_ref_layers(layers: Sequence) -> tuple:
     return arr, keep
 
 
-INT8, FP16 = 0, 1  # NpuPrecision (npu.rs:25-30)
+INT8, FP16, FP32 = 0, 1, 2  # NpuPrecision (npu.rs:25-30); FP32 = the standard path (run_standard, mod.rs:260-331)
 
 
 def round_fp16(x) -> np.ndarray:

@@ -292,7 +292,9 @@ typedef struct {
   int64_t in_f, out_f;              /* Linear: in/out features; Conv: in/out channels */
   int64_t kernel, stride, padding;
   int8_t* wq; float w_scale; int64_t w_len;
-  float* wh;  /* FP16: round_fp16 weights [out, in] / [out, c*k*k]; the raw diagonal for a lone ChannelAffine */
+  float* wh;  /* FP16: round_fp16 weights [out, in] / [out, c*k*k]; the raw diagonal for a lone ChannelAffine.
+                FP32 (standard path): the f32 weights as exported (Linear [in, out], Conv [out, c*k*k]) */
+  float* aff_scale; int64_t aff_len; /* FP32: a ChannelAffine that did not fold (shift in bias) */
   float* bias;
   int act; float act_param;
   /* captures */
@@ -394,6 +396,34 @@ rgref_program* rgref_compile_precision(const rgref_layer* layers, int64_t n_laye
   P->precision = precision;
   P->ops = (ref_op*)calloc((size_t)(nf > 0 ? nf : 1), sizeof(ref_op));
   P->original_layers = n_layers;
+  if (precision == RGREF_FP32) {
+    /* Standard program (mod.rs:164-171): the folded layers, run one by one. */
+    for (int64_t j = 0; j < nf; j++) {
+      folded_layer* f = &F[j];
+      ref_op* op = &P->ops[P->n_ops++];
+      op->kind = f->kind;
+      op->act = f->act; op->act_param = f->act_param;
+      if (f->kind == RGREF_LINEAR) {
+        op->in_f = f->in_f; op->out_f = f->out_f;
+        op->wh = dupf(f->w, f->w_len); op->w_len = f->w_len; op->bias = dupf(f->b, f->b_len);
+        P->fp32_bytes += (f->w_len + f->b_len) * 4;
+      } else if (f->kind == RGREF_CONV2D) {
+        op->in_f = f->in_c; op->out_f = f->out_c;
+        op->kernel = f->k; op->stride = f->s; op->padding = f->p;
+        op->wh = dupf(f->w, f->w_len); op->w_len = f->w_len; op->bias = dupf(f->b, f->b_len);
+        P->fp32_bytes += (f->w_len + f->b_len) * 4;
+      } else if (f->kind == RGREF_CHANNEL_AFFINE) {
+        op->in_f = op->out_f = f->aff_len;
+        op->aff_scale = dupf(f->scale, f->aff_len); op->aff_len = f->aff_len;
+        op->bias = dupf(f->shift, f->aff_len);
+      } else {
+        op->kernel = f->pk; op->stride = f->ps;
+      }
+    }
+    P->npu_bytes = P->fp32_bytes;
+    free_folded(F, nf);
+    return P;
+  }
   int64_t i = 0;
   while (i < nf) {
     int has_act = (i + 1 < nf) && F[i + 1].kind == RGREF_ACTIVATION;
@@ -466,7 +496,7 @@ static void free_caps(ref_op* op) {
 void rgref_program_free(rgref_program* p) {
   if (!p) return;
   for (int64_t i = 0; i < p->n_ops; i++) {
-    free(p->ops[i].wq); free(p->ops[i].wh); free(p->ops[i].bias); free_caps(&p->ops[i]);
+    free(p->ops[i].wq); free(p->ops[i].wh); free(p->ops[i].aff_scale); free(p->ops[i].bias); free_caps(&p->ops[i]);
   }
   free(p->ops); free(p->out); free(p);
 }
@@ -588,6 +618,90 @@ int64_t rgref_program_op_label(const rgref_program* p, int64_t i, char* buf, int
   return n;
 }
 
+/* ================ standard FP32 path (run_standard, mod.rs:260-331) ======== */
+/* Backend matmul C[m,n] = A[m,k] @ B[k,n] as the GPU provider's WGSL shader
+ * orders it (wgpu_impl.rs:20-48): per output a serial f32 sum over k in
+ * order, multiply then add.  (The CPU backend's AVX2/FMA blocking,
+ * cpu.rs:43-160, orders the same products differently.) */
+void rgref_matmul_f32(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c, int parallel) {
+#pragma omp parallel for schedule(dynamic, 4) num_threads(rgref_get_threads()) if (parallel && m * k * n >= 32 * 1024)
+  for (int64_t r = 0; r < m; r++)
+    for (int64_t j = 0; j < n; j++) {
+      float acc = 0.0f;
+      for (int64_t p = 0; p < k; p++) {
+        float prod = a[r * k + p] * b[p * n + j];
+        acc = acc + prod;
+      }
+      c[r * n + j] = acc;
+    }
+}
+
+static int standard_layer(ref_op* op, float** pdata, int64_t* plen, int64_t* shape, int* pnd, int parallel) {
+  float* data = *pdata; int64_t len = *plen; int nd = *pnd;
+  if (op->kind == RGREF_LINEAR) {                                      /* mod.rs:264-273 */
+    int64_t in = op->in_f, out = op->out_f;
+    if (in <= 0 || len % in != 0) { set_err("Linear: input length not a multiple of in_features"); return 1; }
+    int64_t rows = len / in;
+    op->macs = rows * in * out;
+    float* y = (float*)malloc(sizeof(float) * (size_t)(rows * out > 0 ? rows * out : 1));
+    rgref_matmul_f32(data, op->wh, rows, in, out, y, parallel);
+    for (int64_t r = 0; r < rows; r++)
+      for (int64_t c = 0; c < out; c++) y[r * out + c] = y[r * out + c] + op->bias[c];
+    free(data); data = y; len = rows * out; shape[nd - 1] = out;
+  } else if (op->kind == RGREF_CONV2D) {                               /* mod.rs:274-290, kernels.rs:218-265 */
+    if (nd < 4) { set_err("Conv2d: input must be NCHW"); return 1; }
+    int64_t n = shape[0], c = shape[1], h = shape[2], w = shape[3];
+    if (c != op->in_f) { set_err("Conv2d: channel mismatch"); return 1; }
+    int64_t k = op->kernel, s = op->stride, pd = op->padding, O = op->out_f;
+    int64_t oh = rgref_out_size(h, k, s, pd), ow = rgref_out_size(w, k, s, pd);
+    if (oh < 0 || ow < 0) { set_err("Conv2d: kernel larger than padded input"); return 1; }
+    int64_t l = oh * ow, ckk = c * k * k;
+    op->macs = n * O * ckk * l;
+    float* out = (float*)malloc(sizeof(float) * (size_t)(n * O * l > 0 ? n * O * l : 1));
+    float* cols = (float*)malloc(sizeof(float) * (size_t)(ckk * l > 0 ? ckk * l : 1));
+    for (int64_t b = 0; b < n; b++) {
+      rgref_im2col(data + b * c * h * w, c, h, w, k, s, pd, oh, ow, cols);
+      rgref_matmul_f32(op->wh, cols, O, ckk, l, out + b * O * l, parallel); /* W[O,ckk] @ cols[ckk,L] */
+      for (int64_t o = 0; o < O; o++)
+        for (int64_t q = 0; q < l; q++) out[(b * O + o) * l + q] = out[(b * O + o) * l + q] + op->bias[o];
+    }
+    free(cols); free(data); data = out; len = n * O * l;
+    shape[0] = n; shape[1] = O; shape[2] = oh; shape[3] = ow; nd = 4;
+  } else if (op->kind == RGREF_CHANNEL_AFFINE) {                       /* mod.rs:292-306 */
+    if (nd < 2 || shape[1] != op->aff_len) { set_err("ChannelAffine: channel mismatch"); return 1; }
+    int64_t inner = 1;
+    for (int i = 2; i < nd; i++) inner *= shape[i];
+    for (int64_t b = 0; b < shape[0]; b++)
+      for (int64_t ch = 0; ch < op->aff_len; ch++)
+        for (int64_t q = 0; q < inner; q++) {
+          float* v = &data[(b * op->aff_len + ch) * inner + q];
+          float prod = *v * op->aff_scale[ch];
+          *v = prod + op->bias[ch];
+        }
+  } else if (op->kind == RGREF_MAXPOOL2D) {                            /* mod.rs:307-313 */
+    if (nd < 4) { set_err("MaxPool2d: input must be NCHW"); return 1; }
+    int64_t n = shape[0], c = shape[1], h = shape[2], w = shape[3];
+    int64_t oh = rgref_out_size(h, op->kernel, op->stride, 0), ow = rgref_out_size(w, op->kernel, op->stride, 0);
+    if (oh < 0 || ow < 0) { set_err("MaxPool2d: kernel larger than input"); return 1; }
+    float* out = (float*)malloc(sizeof(float) * (size_t)(n * c * oh * ow > 0 ? n * c * oh * ow : 1));
+    rgref_max_pool2d(data, n, c, h, w, op->kernel, op->stride, out, parallel);
+    free(data); data = out; len = n * c * oh * ow; shape[2] = oh; shape[3] = ow; nd = 4;
+  } else if (op->kind == RGREF_FLATTEN) {                              /* mod.rs:314-317 */
+    int64_t rest = 1;
+    for (int i = 1; i < nd; i++) rest *= shape[i];
+    shape[1] = rest; nd = 2;
+  } else if (op->kind == RGREF_ACTIVATION) {                           /* mod.rs:318-322 */
+    for (int64_t i = 0; i < len; i++) data[i] = rgref_act_apply(op->act, op->act_param, data[i]);
+  } else if (op->kind == RGREF_SOFTMAX) {                              /* mod.rs:323-327 */
+    int64_t last = shape[nd - 1];
+    float* y = (float*)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1));
+    if (last > 0) rgref_softmax_rows(data, len / last, last, y);
+    free(data); data = y;
+  }
+  *pdata = data; *plen = len; *pnd = nd;
+  return 0;
+}
+
 /* ======================= execute (npu.rs:296-421) ========================= */
 static void* xmalloc(size_t n) { return malloc(n ? n : 1); }
 
@@ -602,6 +716,10 @@ int rgref_execute(rgref_program* P, const float* x, const int64_t* shape_in, int
     ref_op* op = &P->ops[oi];
     free_caps(op);
     op->macs = 0;
+    if (P->precision == RGREF_FP32) {
+      if (standard_layer(op, &data, &len, shape, &nd, parallel)) { free(data); return 1; }
+      goto op_done;
+    }
     if (op->kind == RGREF_LINEAR) {                                    /* npu.rs:307-318 */
       int64_t in = op->in_f, out = op->out_f;
       if (in <= 0 || len % in != 0) { free(data); set_err("Linear: input length not a multiple of in_features"); return 1; }

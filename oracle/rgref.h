@@ -87,7 +87,8 @@ void rgref_softmax_rows(const float* x, int64_t outer, int64_t size, float* y); 
 
 /* ---- compile / execute (npu.rs:188-276, 296-421) --------------------------- */
 typedef struct rgref_program rgref_program;
-enum { RGREF_INT8 = 0, RGREF_FP16 = 1 }; /* NpuPrecision (npu.rs:25-30) */
+enum { RGREF_INT8 = 0, RGREF_FP16 = 1, RGREF_FP32 = 2 }; /* NpuPrecision (npu.rs:25-30); FP32 = run_standard (mod.rs:260-331) */
+void rgref_matmul_f32(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c, int parallel);
 float rgref_round_fp16(float x);                              /* quantize.rs:50-64 */
 void rgref_round_fp16_array(const float* x, float* y, int64_t n);
 void rgref_fp16_gemm_fused(const float* a, const float* b_t, int64_t m, int64_t k, int64_t n,

@@ -24,7 +24,7 @@ ERR_CAPACITY = 7
 # layer kinds / activation codes / precisions / capture taps
 LAYER_LINEAR, LAYER_CONV2D, LAYER_CHANNEL_AFFINE = 1, 2, 3
 LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_ACTIVATION, LAYER_SOFTMAX = 4, 5, 6, 7
-PRECISION_INT8, PRECISION_FP16 = 0, 1
+PRECISION_INT8, PRECISION_FP16, PRECISION_FP32 = 0, 1, 2
 CAP_QACT, CAP_SCALE, CAP_ACC, CAP_OUT = 0, 1, 2, 3
 
 f32p = ctypes.POINTER(ctypes.c_float)

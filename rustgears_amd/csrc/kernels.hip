@@ -105,14 +105,20 @@ __device__ __forceinline__ float epi_value(int32_t acc, float cs, float b, float
   return act_fixed<ACT>(val, p);
 }
 
+// Operand modes of the MFMA GEMM and the GEMV: i8 (NpuPrecision::Int8),
+// binary16 (NpuPrecision::Fp16) and f32 (the standard FP32 path).
+constexpr int kModeI8 = 0, kModeF16 = 1, kModeF32 = 2;
+
 // One accumulator word to its output.  INT8: the i32 sum, y = act(fl(float(acc)
 // * cs) + b).  FP16: the bits of the f32 sum, y = act(round_fp16(acc + b))
-// (npu.rs:442).
-template <int ACT, bool F16>
+// (npu.rs:442).  FP32: y = act(acc + b) (mod.rs:267-272: matmul, then bias).
+template <int ACT, int MODE>
 __device__ __forceinline__ float epi_word(int32_t w, float cs, float b, float p) {
-  if constexpr (F16) {
+  if constexpr (MODE == kModeF16) {
     const float t = __int_as_float(w) + b;
     return act_fixed<ACT>(rgmath::round_fp16(t), p);
+  } else if constexpr (MODE == kModeF32) {
+    return act_fixed<ACT>(__int_as_float(w) + b, p);
   } else {
     return epi_value<ACT>(w, cs, b, p);
   }
@@ -412,6 +418,92 @@ void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float
   RG_LAUNCH(nlo_to_nchw_kernel, dim3((unsigned)blocks), dim3(256), 0, s, ylo, n, O, L, y);
 }
 
+// ---------------------------------------------------------------------------
+// Standard FP32 path operands: x [M, K] -> A [Mpad, Kpad_f] f32 zero padded
+// (one thread per 4 floats), and im2col in f32 with the reference's column
+// order (kernels.rs:28-96).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pad_rows_f32_kernel(const float* __restrict__ x, int64_t M, int64_t K,
+                                                           int64_t Mpad, int64_t Kpad_f, float* __restrict__ a) {
+  const uint32_t chunks = (uint32_t)(Kpad_f / 4);
+  const int64_t total = Mpad * (int64_t)chunks;
+  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = w / chunks;
+    const uint32_t c0 = (uint32_t)(w - r * chunks) * 4u;
+    float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (r < M) {
+      const float* xr = x + r * K;
+      out.x = c0 < (uint32_t)K ? xr[c0] : 0.0f;
+      out.y = c0 + 1 < (uint32_t)K ? xr[c0 + 1] : 0.0f;
+      out.z = c0 + 2 < (uint32_t)K ? xr[c0 + 2] : 0.0f;
+      out.w = c0 + 3 < (uint32_t)K ? xr[c0 + 3] : 0.0f;
+    }
+    reinterpret_cast<float4*>(a)[w] = out;
+  }
+}
+
+void launch_pad_rows_f32(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_f, float* a, hipStream_t s) {
+  const int64_t chunks = Mpad * (Kpad_f / 4);
+  if (chunks <= 0) return;
+  int64_t blocks = (chunks + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(pad_rows_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_f, a);
+}
+
+__global__ __launch_bounds__(256) void im2col_f32_kernel(const float* __restrict__ x, ConvShape cs, int64_t Mpad,
+                                                         int64_t Kpad_f, float* __restrict__ a) {
+  const uint32_t k = (uint32_t)cs.k, kk2 = k * k, ckk = (uint32_t)cs.C * kk2;
+  const uint32_t L = (uint32_t)(cs.OH * cs.OW), OW = (uint32_t)cs.OW;
+  const uint32_t H = (uint32_t)cs.H, W = (uint32_t)cs.W;
+  const int64_t rows = cs.n * (int64_t)L;
+  const int64_t total = Mpad * Kpad_f;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = e / Kpad_f;
+    const uint32_t kk = (uint32_t)(e - r * Kpad_f);
+    float val = 0.0f;
+    if (r < rows && kk < ckk) {
+      const int64_t img = r / L;
+      const uint32_t p = (uint32_t)(r - img * L);
+      const uint32_t oy = p / OW, ox = p - oy * OW;
+      const uint32_t c = kk / kk2, t = kk - c * kk2, ki = t / k, kj = t - ki * k;
+      const int iy = (int)(oy * (uint32_t)cs.stride + ki) - (int)cs.pad;
+      const int ix = (int)(ox * (uint32_t)cs.stride + kj) - (int)cs.pad;
+      if (iy >= 0 && iy < (int)H && ix >= 0 && ix < (int)W)
+        val = x[img * (int64_t)(cs.C * cs.H * cs.W) + (c * H + (uint32_t)iy) * W + (uint32_t)ix];
+    }
+    a[e] = val;
+  }
+}
+
+void launch_im2col_f32(const float* x, const ConvShape& cs, int64_t Mpad, int64_t Kpad_f, float* a, hipStream_t s) {
+  const int64_t total = Mpad * Kpad_f;
+  if (total <= 0) return;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 16384) blocks = 16384;
+  RG_LAUNCH(im2col_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, cs, Mpad, Kpad_f, a);
+}
+
+// ChannelAffine of the standard path (mod.rs:295-306): channel axis 1,
+// inner = product of the dimensions after it; y = x * scale[ch] + shift[ch]
+// (multiply, then add).
+__global__ __launch_bounds__(256) void channel_affine_kernel(const float* __restrict__ x, int64_t n, int64_t C,
+                                                             int64_t inner, const float* __restrict__ scale,
+                                                             const float* __restrict__ shift, float* __restrict__ y) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t ch = (e / inner) % C;
+    const float prod = x[e] * scale[ch];
+    y[e] = prod + shift[ch];
+  }
+}
+
+void launch_channel_affine(const float* x, int64_t n, int64_t C, int64_t inner, const float* scale, const float* shift,
+                           float* y, hipStream_t s) {
+  if (n <= 0) return;
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  RG_LAUNCH(channel_affine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, n, C, inner, scale, shift, y);
+}
+
 // Lone ChannelAffine in FP16: the diagonal FusedLinear's serial sum has a
 // single non-zero term, the product with the raw scale (npu.rs:254-270,
 // 433-445), so y = round_fp16(fl(round_fp16(x) * scale[c]) + shift[c]).
@@ -610,14 +702,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
-template <int ACT, bool CAP, bool F16>
+template <int ACT, bool CAP, int MODE>
 __device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int rows, float* yp, int32_t* ap, int64_t N,
                                                       float cs, float b, float p, int lane) {
   uint32_t amax = 0;
 #pragma unroll 1
   for (int r = 0; r < rows; r++) {
     const int32_t a = slab[r * big::SLAB_LD + lane];
-    const float v = epi_word<ACT, F16>(a, cs, b, p);
+    const float v = epi_word<ACT, MODE>(a, cs, b, p);
     *yp = v;
     yp += N;
     if (CAP) {
@@ -634,7 +726,7 @@ __device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int r
 // time and stores it row-major: lane l owns column n0 + wn*64 + l, so each
 // store instruction writes 256 contiguous bytes.  The bias and scale were
 // loaded before the K loop.
-template <int ACT, bool CAP, int FM, bool F16>
+template <int ACT, bool CAP, int FM, int MODE>
 __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                  int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                  int wave, int wm, int wn, int lane) {
@@ -654,18 +746,18 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
     const int rows = col_ok ? (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16) : 0;
     float* yp = ep.y + row0 * N + col;
     int32_t* ap = CAP ? ep.acc_out + row0 * N + col : nullptr;
-    const uint32_t a = big_epilogue_slab<ACT, CAP, F16>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
+    const uint32_t a = big_epilogue_slab<ACT, CAP, MODE>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
     amax = a > amax ? a : amax;
   }
   return amax;
 }
 
-template <int ACT, int FM, bool F16>
+template <int ACT, int FM, int MODE>
 __device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                      int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                      int wave, int wm, int wn, int lane) {
-  return ep.acc_out ? big_epilogue<ACT, true, FM, F16>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
-                    : big_epilogue<ACT, false, FM, F16>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
+  return ep.acc_out ? big_epilogue<ACT, true, FM, MODE>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane)
+                    : big_epilogue<ACT, false, FM, MODE>(smem, acc, m0, n0, M, N, cs, b, ep, wave, wm, wn, lane);
 }
 
 // Split K: gridDim.y > 1 gives block (x, y) the K steps [y*ks, (y+1)*ks) and
@@ -676,7 +768,7 @@ __device__ __forceinline__ uint32_t big_epilogue_any(int8_t* smem, const v4i (&a
 // whose per-lane operand layout matches the i8 instruction's byte for byte,
 // so the DMA ring, swizzle and LDS reads are shared.  The f32 sums travel in
 // the same 32-bit accumulator words.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, bool F16>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int MODE>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, int64_t M, int64_t N, int64_t Kpad, int tiles_m,
     int tiles_n, Epilogue ep, int ks, int32_t* __restrict__ ws) {
@@ -701,7 +793,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
   // Partial of the input absmax; folded after the K loop so the fold does not
   // wait on the prologue DMA.  (FP16 has no activation scale.)
   uint32_t absmax_part = 0;
-  if constexpr (!F16) absmax_part = tensor_absmax_part(ep.absmax_in);
+  if constexpr (MODE == kModeI8) absmax_part = tensor_absmax_part(ep.absmax_in);
 
   // DMA addressing: uniform tile base pointers plus 32-bit per-lane offsets.
   // Wave w fills A rows [16 IA w, 16 IA (w+1)) and B rows [16 IB w, ...).
@@ -770,11 +862,20 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
     for (int i = 0; i < FM; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        if constexpr (F16)
+        if constexpr (MODE == kModeF16) {
           acc[i][j] = __builtin_bit_cast(
               v4i, __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, af[i]), __builtin_bit_cast(v8h, bf[j]),
                                                            __builtin_bit_cast(v4f, acc[i][j]), 0, 0, 0));
-        else
+        } else if constexpr (MODE == kModeF32) {
+          // Each lane's 16 bytes are 4 floats of its row, k = 4 (lane / 16) + c;
+          // one v_mfma_f32_16x16x4_f32 per c covers the step's 16 k values
+          // (the same products, grouped by c).
+          v4f a4 = __builtin_bit_cast(v4f, acc[i][j]);
+          const v4f fa = __builtin_bit_cast(v4f, af[i]), fb = __builtin_bit_cast(v4f, bf[j]);
+#pragma unroll
+          for (int c = 0; c < 4; c++) a4 = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[c], fb[c], a4, 0, 0, 0);
+          acc[i][j] = __builtin_bit_cast(v4i, a4);
+        } else
           acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
       }
     st_rd = st_rd == (uint32_t)((STAGES - 1) * ST) ? 0 : st_rd + ST;
@@ -797,9 +898,10 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
     (void)absmax_part;
     return;
   }
-  const float cs = F16 ? 1.0f : rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
+  const float cs =
+      MODE != kModeI8 ? 1.0f : rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
   uint32_t amax = 0;
-#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV, FM, F16>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
+#define RG_BIG_EPI(ACTV) big_epilogue_any<ACTV, FM, MODE>(smem, acc, m0, n0, M, N, cs, bias_v, ep, wave, wm, wn, lane)
   switch (ep.act) {
     case rgmath::ACT_RELU: amax = RG_BIG_EPI(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: amax = RG_BIG_EPI(rgmath::ACT_SIGMOID); break;
@@ -818,17 +920,17 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
 
 // Split-K epilogue: the S partial sums added in slice order, then the fused
 // epilogue (INT8: exact i32 sum; FP16: f32 sum).
-template <int ACT, bool F16>
+template <int ACT, int MODE>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, int64_t Mpad, int64_t Npad, Epilogue ep) {
   float cs = 1.0f;
-  if constexpr (!F16) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int64_t n4 = Npad / 4, total = M * n4;
   uint32_t amax = 0;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / n4, c0 = (e - row * n4) * 4;
     v4i sum = v4i{0, 0, 0, 0};
-    if constexpr (F16) {
+    if constexpr (MODE != kModeI8) {
       v4f f = v4f{0.0f, 0.0f, 0.0f, 0.0f};
       for (int sp = 0; sp < S; sp++)
         f += __builtin_bit_cast(v4f, *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0));
@@ -840,7 +942,7 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __r
     for (int q = 0; q < 4; q++) {
       const int64_t col = c0 + q;
       if (col < N) {
-        const float v = epi_word<ACT, F16>(sum[q], cs, ep.bias[col], ep.act_param);
+        const float v = epi_word<ACT, MODE>(sum[q], cs, ep.bias[col], ep.act_param);
         ep.y[row * N + col] = v;
         if (ep.acc_out) ep.acc_out[row * N + col] = sum[q];
         const uint32_t k = rgmath::absmax_key(v);
@@ -854,14 +956,14 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __r
   }
 }
 
-template <bool F16>
+template <int MODE>
 static void launch_splitk_epilogue(const int32_t* ws, int S, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                                    const Epilogue& ep, hipStream_t s) {
   int64_t blocks = (M * (Npad / 4) + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   if (blocks < 1) blocks = 1;
 #define RG_SKE(ACTV) \
-  RG_LAUNCH((splitk_epilogue_kernel<ACTV, F16>), dim3((unsigned)blocks), dim3(256), 0, s, ws, S, M, N, Mpad, Npad, ep)
+  RG_LAUNCH((splitk_epilogue_kernel<ACTV, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, ws, S, M, N, Mpad, Npad, ep)
   switch (ep.act) {
     case rgmath::ACT_RELU: RG_SKE(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: RG_SKE(rgmath::ACT_SIGMOID); break;
@@ -874,13 +976,13 @@ static void launch_splitk_epilogue(const int32_t* ws, int S, int64_t M, int64_t 
 #undef RG_SKE
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, bool F16>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int MODE>
 static void launch_big(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                        int64_t Kpad, const Epilogue& ep, int splits, int32_t* ws, hipStream_t s) {
   const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
   const int nk = (int)(Kpad / big::BK);
   const int ks = (nk + splits - 1) / splits;
-  RG_LAUNCH((gemm_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, F16>), dim3((unsigned)(tm * tn), (unsigned)splits),
+  RG_LAUNCH((gemm_big_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, MODE>), dim3((unsigned)(tm * tn), (unsigned)splits),
             dim3(WAVES_M * WAVES_N * 64), 0, s, A, B, M, N, Kpad, tm, tn, ep, ks, ws);
 }
 
@@ -910,33 +1012,39 @@ int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad) {
   return g.kind == 2 && g.splits > 1 ? (int64_t)g.splits * Mpad * Npad * 4 : 0;
 }
 
-template <bool F16>
+template <int MODE>
 static void launch_gemm_t(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                           int64_t Kpad, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
   if (Kpad % big::BK || Mpad % 128 || Npad % 128 || Kpad <= 0)
     throw std::logic_error("GEMM operands must be padded to 128 rows and 64-byte K steps");
   const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
   if (g.kind == 0) {
-    launch_big<256, 256, 2, 4, 4, 1, 8, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<256, 256, 2, 4, 4, 1, 8, MODE>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   } else if (g.kind == 1) {
-    launch_big<256, 128, 2, 2, 3, 2, 8, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<256, 128, 2, 2, 3, 2, 8, MODE>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   } else if (g.splits > 1 && ws && ws_bytes >= (int64_t)g.splits * Mpad * Npad * 4) {
-    launch_big<128, 128, 2, 2, 4, 2, 4, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, g.splits, ws, s);
-    launch_splitk_epilogue<F16>(ws, g.splits, M, N, Mpad, Npad, ep, s);
+    launch_big<128, 128, 2, 2, 4, 2, 4, MODE>(A, B, M, N, Mpad, Npad, Kpad, ep, g.splits, ws, s);
+    launch_splitk_epilogue<MODE>(ws, g.splits, M, N, Mpad, Npad, ep, s);
   } else {
-    launch_big<128, 128, 2, 2, 4, 2, 4, F16>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
+    launch_big<128, 128, 2, 2, 4, 2, 4, MODE>(A, B, M, N, Mpad, Npad, Kpad, ep, 1, nullptr, s);
   }
 }
 
 void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
-  launch_gemm_t<false>(A, B, M, N, Mpad, Npad, Kpad, ep, ws, ws_bytes, s);
+  launch_gemm_t<kModeI8>(A, B, M, N, Mpad, Npad, Kpad, ep, ws, ws_bytes, s);
+}
+
+void launch_gemm_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                     int64_t Kpad_f, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
+  launch_gemm_t<kModeF32>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Mpad, Npad,
+                          4 * Kpad_f, ep, ws, ws_bytes, s);
 }
 
 void launch_gemm_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                      int64_t Kpad_h, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s) {
-  launch_gemm_t<true>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Mpad, Npad,
-                      2 * Kpad_h, ep, ws, ws_bytes, s);
+  launch_gemm_t<kModeF16>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Mpad, Npad,
+                          2 * Kpad_h, ep, ws, ws_bytes, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1030,7 +1138,7 @@ constexpr int pow2_at_least(int v) { return v <= 1 ? 1 : 2 * pow2_at_least((v + 
 // chunk), the partial sums are f32 from v_dot2_f32_f16 (exact products; the
 // summation order differs from the reference's serial one), and the
 // epilogue is act(round_fp16(acc + bias)).
-template <int MR, int R, int U, bool F16>
+template <int MR, int R, int U, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                    int64_t N, int64_t groups, int64_t Kpad, Epilogue ep) {
   constexpr int S = pow2_at_least(MR * R);
@@ -1038,7 +1146,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A,
   const int lane = threadIdx.x & 63;
   const int64_t waves = (int64_t)gridDim.x * 4;
   float cs = 1.0f;
-  if constexpr (!F16) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int sidx = lane / SPREAD;
   const int om = sidx / R, orr = sidx % R;
   const bool owner = (lane % SPREAD) == 0 && sidx < MR * R;
@@ -1081,7 +1189,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A,
 #pragma unroll
           for (int r = 0; r < R; r++) {
             int32_t a = acc[m * R + r];
-            if constexpr (F16) {
+            if constexpr (MODE == kModeF32) {
+              const v4f xf = __builtin_bit_cast(v4f, xv), wf = __builtin_bit_cast(v4f, w[u][r]);
+              float f = __int_as_float(a);
+#pragma unroll
+              for (int q = 0; q < 4; q++) f = __builtin_fmaf(xf[q], wf[q], f);
+              a = __float_as_int(f);
+            } else if constexpr (MODE == kModeF16) {
               const v8h xh = __builtin_bit_cast(v8h, xv), wh = __builtin_bit_cast(v8h, w[u][r]);
               float f = __int_as_float(a);
 #pragma unroll
@@ -1098,12 +1212,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A,
           }
         }
     }
-    const int32_t mine = wave_reduce_scatter<S, F16>(acc, lane);
+    const int32_t mine = wave_reduce_scatter<S, MODE != kModeI8>(acc, lane);
     // INT8: (acc as f32) * cs + bias with separate roundings, as in
     // epi_value.  FP16: round_fp16(acc + bias).
     float pre;
-    if constexpr (F16) {
+    if constexpr (MODE == kModeF16) {
       pre = rgmath::round_fp16(__int_as_float(mine) + bias_v);
+    } else if constexpr (MODE == kModeF32) {
+      pre = __int_as_float(mine) + bias_v;
     } else {
       const float prod = (float)mine * cs;
       pre = prod + bias_v;
@@ -1132,19 +1248,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(const int8_t* __restrict__ A,
 }
 
 
-template <int MR, int R, int U, bool F16>
+template <int MR, int R, int U, int MODE>
 void launch_gemv_t(const int8_t* A, const int8_t* B, int64_t N, int64_t Npad, int64_t Kpad, const Epilogue& ep,
                    hipStream_t s, int64_t max_blocks) {
-  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, R, U, F16>);
+  const void* fn = reinterpret_cast<const void*>(&gemv_kernel<MR, R, U, MODE>);
   static const int64_t cap = resident_blocks(fn);
   const int64_t groups = Npad / R;  // Npad is a multiple of 256, so of every R used
   int64_t blocks = (groups + 3) / 4;
   const int64_t lim = max_blocks > 0 ? max_blocks : cap;
   if (blocks > lim) blocks = lim;
-  RG_LAUNCH((gemv_kernel<MR, R, U, F16>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
+  RG_LAUNCH((gemv_kernel<MR, R, U, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, N, groups, Kpad, ep);
 }
 
-template <bool F16>
+template <int MODE>
 static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                             const Epilogue& ep, hipStream_t s) {
   // (R, U) from a sweep on the decode shapes (8192 x 28672 and 28672 x
@@ -1152,34 +1268,40 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
   // favour 8 rows per wave.
   const bool long_k = Kpad >= 16384;
   switch (M) {
-    case 1: launch_gemv_t<1, 4, 4, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 2: launch_gemv_t<2, 4, 4, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 3: launch_gemv_t<3, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
-    case 4: launch_gemv_t<4, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 1: launch_gemv_t<1, 4, 4, MODE>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 2: launch_gemv_t<2, 4, 4, MODE>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 3: launch_gemv_t<3, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0); break;
+    case 4: launch_gemv_t<4, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0); break;
     case 5:
-      long_k ? launch_gemv_t<5, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<5, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<5, 8, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<5, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     case 6:
-      long_k ? launch_gemv_t<6, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<6, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<6, 8, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<6, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     case 7:
-      long_k ? launch_gemv_t<7, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<7, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<7, 8, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<7, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
     default:
-      long_k ? launch_gemv_t<8, 8, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<8, 4, 1, F16>(A, B, N, Npad, Kpad, ep, s, 0);
+      long_k ? launch_gemv_t<8, 8, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0) : launch_gemv_t<8, 4, 1, MODE>(A, B, N, Npad, Kpad, ep, s, 0);
       break;
   }
 }
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
-  launch_gemv_any<false>(A, B, M, N, Npad, Kpad, ep, s);
+  launch_gemv_any<kModeI8>(A, B, M, N, Npad, Kpad, ep, s);
+}
+
+void launch_gemv_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_f,
+                     const Epilogue& ep, hipStream_t s) {
+  launch_gemv_any<kModeF32>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Npad,
+                            4 * Kpad_f, ep, s);
 }
 
 void launch_gemv_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_h,
                      const Epilogue& ep, hipStream_t s) {
-  launch_gemv_any<true>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Npad, 2 * Kpad_h,
-                        ep, s);
+  launch_gemv_any<kModeF16>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N, Npad,
+                            2 * Kpad_h, ep, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -88,7 +88,7 @@ static std::string act_display(int act, float p) {
   return "?";
 }
 
-enum OpKind { OP_LINEAR = 1, OP_CONV = 2, OP_POOL = 4, OP_FLATTEN = 5, OP_ACT = 6, OP_SOFTMAX = 7 };
+enum OpKind { OP_LINEAR = 1, OP_CONV = 2, OP_AFFINE = 3, OP_POOL = 4, OP_FLATTEN = 5, OP_ACT = 6, OP_SOFTMAX = 7 };
 
 struct Op {
   int kind = 0;
@@ -98,7 +98,7 @@ struct Op {
   float act_param = 0.0f;
   std::vector<int8_t> wq;  // [out, K] as the reference holds it (INT8)
   float w_scale = 1.0f;
-  std::vector<float> wh;   // FP16: round_fp16 weights [out, K] (npu.rs:210, 232)
+  std::vector<float> wh;   // FP16: round_fp16 weights [out, K] (npu.rs:210, 232); FP32: the f32 weights [out, K]
   bool diag = false;       // FP16 lone ChannelAffine: elementwise, scale kept as is (npu.rs:254-270)
   std::vector<float> diag_scale;
   std::vector<float> bias;
@@ -337,12 +337,110 @@ static std::string op_label(const Op& op) {
   return buf;
 }
 
+// FP32 weights [Npad, Kpad_f] (Linear transposed to [out, in], Conv [O, c*k*k]), zero padded.
+static void upload_weights_f32(Op& op, hipStream_t s) {
+  std::vector<float> bpad((size_t)std::max<int64_t>(op.Npad, (int64_t)op.bias.size()), 0.0f);
+  std::memcpy(bpad.data(), op.bias.data(), sizeof(float) * op.bias.size());
+  op.d_bias.ensure(bpad.size() * sizeof(float));
+  RG_HIP(hipMemcpyAsync(op.d_bias.p, bpad.data(), bpad.size() * sizeof(float), hipMemcpyHostToDevice, s));
+  if (op.kind == OP_AFFINE) {
+    op.d_scale.ensure(op.diag_scale.size() * sizeof(float));
+    RG_HIP(hipMemcpyAsync(op.d_scale.p, op.diag_scale.data(), op.diag_scale.size() * sizeof(float),
+                          hipMemcpyHostToDevice, s));
+  } else {
+    std::vector<float> w((size_t)(op.Npad * op.Kpad), 0.0f);
+    for (int64_t r = 0; r < op.out_f; r++)
+      std::memcpy(&w[(size_t)(r * op.Kpad)], &op.wh[(size_t)(r * op.K)], sizeof(float) * (size_t)op.K);
+    op.d_w.ensure(w.size() * sizeof(float));
+    RG_HIP(hipMemcpyAsync(op.d_w.p, w.data(), w.size() * sizeof(float), hipMemcpyHostToDevice, s));
+  }
+  RG_HIP(hipStreamSynchronize(s));
+}
+
+// The standard FP32 program of ExecutionProvider::Gpu(i): the folded layers
+// (InferenceSession::from_layers, mod.rs:168-171) run one by one as
+// run_standard does (mod.rs:260-331) -- no Linear/Activation fusion, and a
+// ChannelAffine that did not fold stays an elementwise affine.
+static void compile_standard(rgnpu_program* P, const std::vector<FLayer>& F) {
+  for (const FLayer& f : F) {
+    auto op = std::make_unique<Op>();
+    char buf[160];
+    switch (f.spec.kind) {
+      case RGNPU_LAYER_LINEAR: {
+        op->kind = OP_LINEAR;
+        op->in_f = f.spec.in_features;
+        op->out_f = f.spec.out_features;
+        op->K = op->in_f;
+        op->wh.resize((size_t)(op->in_f * op->out_f));
+        for (int64_t r = 0; r < op->in_f; r++)
+          for (int64_t c = 0; c < op->out_f; c++) op->wh[(size_t)(c * op->in_f + r)] = f.w[(size_t)(r * op->out_f + c)];
+        op->bias = f.b;
+        op->Npad = round_up(op->out_f, kRowPad);
+        op->Kpad = round_up(op->K, kKPadF32);
+        snprintf(buf, sizeof buf, "GPU::Linear(%lld->%lld)", (long long)op->in_f, (long long)op->out_f);
+        break;
+      }
+      case RGNPU_LAYER_CONV2D:
+        op->kind = OP_CONV;
+        op->in_f = f.spec.in_channels;
+        op->out_f = f.spec.out_channels;
+        op->k = f.spec.kernel;
+        op->s = f.spec.stride;
+        op->p = f.spec.padding;
+        op->K = op->in_f * op->k * op->k;
+        op->wh = f.w;  // [O, c*k*k]
+        op->bias = f.b;
+        op->Npad = round_up(op->out_f, 128);
+        op->Kpad = round_up(op->K, kKPadF32);
+        snprintf(buf, sizeof buf, "GPU::Conv2d(%lld->%lld, k=%lld)", (long long)op->in_f, (long long)op->out_f,
+                 (long long)op->k);
+        break;
+      case RGNPU_LAYER_CHANNEL_AFFINE:
+        op->kind = OP_AFFINE;
+        op->in_f = op->out_f = (int64_t)f.scale.size();
+        op->diag_scale = f.scale;
+        op->bias = f.shift;
+        snprintf(buf, sizeof buf, "GPU::ChannelAffine(%lld)", (long long)op->in_f);
+        break;
+      case RGNPU_LAYER_MAXPOOL2D:
+        op->kind = OP_POOL;
+        op->k = f.spec.pool_kernel;
+        op->s = f.spec.pool_stride;
+        snprintf(buf, sizeof buf, "GPU::MaxPool2d(k=%lld)", (long long)op->k);
+        break;
+      case RGNPU_LAYER_FLATTEN:
+        op->kind = OP_FLATTEN;
+        snprintf(buf, sizeof buf, "GPU::Flatten");
+        break;
+      case RGNPU_LAYER_ACTIVATION:
+        op->kind = OP_ACT;
+        op->act = f.spec.act;
+        op->act_param = f.spec.act_param;
+        snprintf(buf, sizeof buf, "GPU::Act(%s)", act_display(op->act, op->act_param).c_str());
+        break;
+      default:
+        op->kind = OP_SOFTMAX;
+        snprintf(buf, sizeof buf, "GPU::Softmax");
+        break;
+    }
+    if (op->kind == OP_LINEAR || op->kind == OP_CONV) P->fp32_bytes += (int64_t)(f.w.size() + f.b.size()) * 4;
+    if (op->kind == OP_LINEAR || op->kind == OP_CONV || op->kind == OP_AFFINE) upload_weights_f32(*op, P->stream);
+    op->label = buf;
+    P->ops.push_back(std::move(op));
+  }
+  P->npu_bytes = P->fp32_bytes;
+}
+
 // npu::compile (npu.rs:188-276).
 static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
   const bool f16 = P->precision == RGNPU_PRECISION_FP16;
   for (int64_t i = 0; i < n; i++) check_layer(layers[i], i);
   P->original_layers = n;
   std::vector<FLayer> F = fold_batch_norm(layers, n);
+  if (P->precision == RGNPU_PRECISION_FP32) {
+    compile_standard(P, F);
+    return;
+  }
   size_t i = 0;
   while (i < F.size()) {
     const bool has_act = i + 1 < F.size() && F[i + 1].spec.kind == RGNPU_LAYER_ACTIVATION;
@@ -530,6 +628,12 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         cur = {cur[0], rest};
         break;
       }
+      case OP_AFFINE: {  // mod.rs:295-306: channels on axis 1
+        if (cur.size() < 2 || cur[1] != op.in_f)
+          throw Error(RGNPU_ERR_SHAPE, "ChannelAffine(" + std::to_string(op.in_f) + "): input axis 1 must have " +
+                                           std::to_string(op.in_f) + " channels");
+        break;
+      }
       default:
         break;
     }
@@ -567,12 +671,13 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR && op.kind != OP_CONV) continue;
-    if (P->precision == RGNPU_PRECISION_FP16) {
-      // No activation quantization: binary16 operands, the split-K
-      // workspace, and the conv's [n*L, O] GEMM output.
+    if (P->precision != RGNPU_PRECISION_INT8) {
+      // No activation quantization: binary16 (FP16) or f32 (FP32) operands,
+      // the split-K workspace, and the conv's [n*L, O] GEMM output.
       if (op.diag) continue;
-      plan->q_bytes = std::max(plan->q_bytes, (size_t)(pl.Mpad * op.Kpad) * 2);
-      if (!pl.gemv) plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, 2 * op.Kpad));
+      const int64_t es = P->precision == RGNPU_PRECISION_FP16 ? 2 : 4;
+      plan->q_bytes = std::max(plan->q_bytes, (size_t)(pl.Mpad * op.Kpad * es));
+      if (!pl.gemv) plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, es * op.Kpad));
       if (op.kind == OP_CONV) plan->ylo_elems = std::max(plan->ylo_elems, (size_t)(pl.rows * op.out_f));
       continue;
     }
@@ -712,6 +817,7 @@ static void op_times(const rgnpu_program* P, const Plan& plan, const hipEvent_t*
 static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipEvent_t* ev, bool timed) {
   hipStream_t s = P->stream;
   const bool f16 = P->precision == RGNPU_PRECISION_FP16;
+  const bool f32 = P->precision == RGNPU_PRECISION_FP32;
   const bool cap = P->capture;
   struct SinkOff {
     ~SinkOff() { set_launch_events(nullptr, 0); }
@@ -755,6 +861,23 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     uint32_t* emit = pl.emit_slot >= 0 ? slots + pl.emit_slot : nullptr;
     switch (op.kind) {
       case OP_LINEAR: {
+        if (f32) {  // mod.rs:263-273: matmul, then the bias
+          pre = launch_events_used();
+          if (pl.rows > 0) {
+            float* a = plan.q.as<float>();
+            launch_pad_rows_f32(in, pl.rows, op.K, pl.Mpad, op.Kpad, a, s);
+            Epilogue ep;
+            ep.bias = op.d_bias.as<float>();
+            ep.y = out;
+            pre = launch_events_used();
+            if (pl.gemv)
+              launch_gemv_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+            else
+              launch_gemm_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                              plan.ws.as<int32_t>(), plan.ws_bytes, s);
+          }
+          break;
+        }
         if (f16) {  // npu.rs:315
           pre = launch_events_used();
           if (op.diag) {
@@ -805,6 +928,21 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
       }
       case OP_CONV: {
         const ConvShape& c = pl.cs;
+        if (f32) {  // mod.rs:274-290: conv2d_forward (im2col + matmul), then the bias
+          pre = launch_events_used();
+          if (pl.rows > 0) {
+            float* a = plan.q.as<float>();
+            launch_im2col_f32(in, c, pl.Mpad, op.Kpad, a, s);
+            Epilogue ep;
+            ep.bias = op.d_bias.as<float>();
+            ep.y = plan.ylo.as<float>();
+            pre = launch_events_used();
+            launch_gemm_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+                            plan.ws.as<int32_t>(), plan.ws_bytes, s);
+            launch_nlo_to_nchw(plan.ylo.as<float>(), c.n, op.out_f, c.OH * c.OW, out, s);
+          }
+          break;
+        }
         if (f16) {  // npu.rs:341-376: im2col, GEMM, transpose per image
           pre = launch_events_used();
           if (pl.rows > 0) {
@@ -862,6 +1000,13 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         pre = launch_events_used();
         launch_activation(in, out, pl.in_len, op.act, op.act_param, emit, s);
         break;
+      case OP_AFFINE: {
+        int64_t inner = 1;
+        for (size_t d = 2; d < pl.in_shape.size(); d++) inner *= pl.in_shape[d];
+        pre = launch_events_used();
+        launch_channel_affine(in, pl.in_len, op.in_f, inner, op.d_scale.as<float>(), op.d_bias.as<float>(), out, s);
+        break;
+      }
       case OP_SOFTMAX: {
         const int64_t last = pl.in_shape.back();
         pre = launch_events_used();
@@ -961,7 +1106,7 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
   if (!out) throw Error(RGNPU_ERR_INVALID, "out is NULL");
   *out = nullptr;
   if (n_layers < 0 || (n_layers > 0 && !layers)) throw Error(RGNPU_ERR_INVALID, "invalid layer list");
-  if (precision != RGNPU_PRECISION_INT8 && precision != RGNPU_PRECISION_FP16)
+  if (precision != RGNPU_PRECISION_INT8 && precision != RGNPU_PRECISION_FP16 && precision != RGNPU_PRECISION_FP32)
     throw Error(RGNPU_ERR_INVALID, "unknown precision");
   int count = 0;
   RG_HIP(hipGetDeviceCount(&count));
@@ -1148,6 +1293,14 @@ int64_t rgnpu_program_summary(const rgnpu_program* P, char* buf, int64_t cap) {
     names += P->ops[i]->label;
   }
   char head[512];
+  if (P->precision == RGNPU_PRECISION_FP32) {
+    // compilation_report of a Standard program (mod.rs:198-204)
+    snprintf(head, sizeof head, "InferenceSession [provider = GPU:%d (FP32), device = gpu:%d, ops = %zu (from %lld raw layers)]",
+             P->device, P->device, P->ops.size(), (long long)P->original_layers);
+    const std::string st(head);
+    if (buf && cap > 0) snprintf(buf, (size_t)cap, "%s", st.c_str());
+    return (int64_t)st.size();
+  }
   snprintf(head, sizeof head,
            "InferenceSession [provider = MI355X (%s), layers: %lld -> %zu fused ops, weights: %lld B -> %lld B (%.2fx "
            "compression)]\n  Pipeline: ",

@@ -11,6 +11,7 @@ namespace rgnpu {
 constexpr int64_t kRowPad = 256;   // Linear output features and activation rows
 constexpr int64_t kKPad = 128;     // reduction dimension (bytes)
 constexpr int64_t kKPadHalf = 32;  // FP16 reduction dimension (binary16 elements: one 64-byte K step)
+constexpr int64_t kKPadF32 = 16;   // FP32 reduction dimension (f32 elements: one 64-byte K step)
 constexpr int64_t kConvOPad = 32;  // conv output channels
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
@@ -126,6 +127,21 @@ void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float
 // Lone ChannelAffine: y = round_fp16(fl(round_fp16(x) * scale[c]) + shift[c]), c = index % C.
 void launch_affine_f16(const float* x, int64_t n, int64_t C, const float* scale, const float* shift, float* y,
                        hipStream_t s);
+
+// ---- Standard FP32 path (ExecutionProvider::Gpu, run_standard) ------------
+// f32 MFMA GEMM (v_mfma_f32_16x16x4_f32: full f32 products and sums, no
+// reduced-precision inputs), epilogue y = act(acc + bias); A [Mpad, Kpad_f],
+// B [Npad, Kpad_f], Kpad_f a multiple of 16 (one 64-byte K step).
+void launch_gemm_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                     int64_t Kpad_f, const Epilogue& ep, int32_t* ws, int64_t ws_bytes, hipStream_t s);
+void launch_gemv_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_f,
+                     const Epilogue& ep, hipStream_t s);
+void launch_pad_rows_f32(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_f, float* a,
+                         hipStream_t s);
+void launch_im2col_f32(const float* x, const ConvShape& cs, int64_t Mpad, int64_t Kpad_f, float* a, hipStream_t s);
+// y = x * scale[ch] + shift[ch] with ch = (index / inner) % C.
+void launch_channel_affine(const float* x, int64_t n, int64_t C, int64_t inner, const float* scale,
+                           const float* shift, float* y, hipStream_t s);
 
 // Max pool (kernels.rs:165-213 semantics) with optional absmax of the output.
 void launch_maxpool(const float* x, float* y, int64_t n, int64_t C, int64_t H, int64_t W,

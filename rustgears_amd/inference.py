@@ -236,6 +236,12 @@ class ExecutionProvider:
         return ExecutionProvider("mi355x", NpuPrecision.Fp16, device)
 
     @staticmethod
+    def Gpu(index: int = 0) -> "ExecutionProvider":
+        """ExecutionProvider::Gpu(i): the standard FP32 path (run_standard,
+        mod.rs:260-331), executed on MI355X device `index`."""
+        return ExecutionProvider("gpu", None, index)
+
+    @staticmethod
     def Npu(precision: NpuPrecision) -> "ExecutionProvider":
         return ExecutionProvider("npu", precision)
 
@@ -357,13 +363,17 @@ class InferenceSession:
 
     @classmethod
     def from_layers(cls, raw_layers: Sequence[AnyLayer], provider: ExecutionProvider) -> "InferenceSession":
-        """mod.rs:162-180 with the Mi355x variant -> rgnpu_program_create."""
-        if provider.kind != "mi355x":
+        """mod.rs:162-180 with the Mi355x variant -> rgnpu_program_create; the
+        Gpu(i) variant builds the standard FP32 program on MI355X device i."""
+        if provider.kind not in ("mi355x", "gpu"):
             raise NotImplementedError(
-                f"provider {provider} runs in the reference; this package provides ExecutionProvider.Mi355x")
+                f"provider {provider} runs in the reference; this package provides ExecutionProvider.Mi355x and Gpu")
         arr, keep = to_c_layers(raw_layers)
         h = ctypes.c_void_p()
-        prec = N.PRECISION_INT8 if provider.precision is NpuPrecision.Int8 else N.PRECISION_FP16
+        if provider.kind == "gpu":
+            prec = N.PRECISION_FP32
+        else:
+            prec = N.PRECISION_INT8 if provider.precision is NpuPrecision.Int8 else N.PRECISION_FP16
         N.check(N.lib().rgnpu_program_create(arr, len(raw_layers), prec, provider.index, ctypes.byref(h)))
         del keep
         return cls(provider, list(raw_layers), h.value)
@@ -454,7 +464,10 @@ class InferenceSession:
         N.check(N.lib().rgnpu_program_set_profiling(self._h, level))
 
     def last_npu_profile(self) -> Optional[NpuProfile]:
-        """mod.rs:193-195."""
+        """mod.rs:193-195 (None for the standard FP32 path, which records no
+        NPU profile)."""
+        if self._provider.kind == "gpu":
+            return None
         hdr = N.CProfile()
         recs = (N.COpRecord * 256)()
         st = N.lib().rgnpu_program_profile(self._h, ctypes.byref(hdr), recs, 256)

@@ -501,3 +501,68 @@ def test_fp16_conv_is_im2col_gemm(ref):
         cols = _im2col_brute(x[i], c, h, w, k, 1, 1)  # [ckk, L]
         ylo = ref.fp16_gemm_fused(cols.T.copy(), ref.round_fp16(wt.reshape(o, -1)), b)
         assert_bitexact_f32(y[i], ylo.T.reshape(o, h, w))
+
+
+# ---- standard FP32 path (run_standard, mod.rs:260-331) ----------------------
+@pytest.mark.parametrize("m,k,n", [(3, 5, 4), (2, 17, 3), (1, 1, 1)])
+def test_standard_matmul_serial_order(ref, m, k, n):
+    """rgref_matmul_f32: per output a serial float32 sum over k in order,
+    multiply then add (the WGSL shader's order, wgpu_impl.rs:20-48)."""
+    rng = np.random.default_rng(m + 10 * k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    c = np.empty((m, n), np.float32)
+    ref.lib().rgref_matmul_f32(ref._fp(a), ref._fp(b), m, k, n, ref._fp(c), 0)
+    want = np.empty((m, n), np.float32)
+    for r in range(m):
+        for j in range(n):
+            acc = np.float32(0.0)
+            for p in range(k):
+                acc = np.float32(acc + np.float32(a[r, p] * b[p, j]))
+            want[r, j] = acc
+    assert_bitexact_f32(c, want)
+
+
+def test_standard_program_linear_bn_relu(ref, rg):
+    """Standard program: BN folded like the NPU compile (mod.rs:168-171), then
+    matmul with the exported [in, out] weights, the bias added separately,
+    and ReLU as its own layer."""
+    from rustgears_amd import nn
+    rg.manual_seed(77)
+    lin, bn = nn.Linear(6, 5), nn.BatchNorm1d(5)
+    bn.running_mean = rg.randn([5])
+    bn.running_var = rg.uniform([5], 0.5, 1.5)
+    layers = nn.Sequential().add(lin).add(bn).add(nn.Relu()).export()
+    aff = layers[1]
+    w = (lin.weight * aff.scale[None, :]).astype(np.float32)
+    b = ((lin.bias * aff.scale).astype(np.float32) + aff.shift).astype(np.float32)
+    x = rg.randn([3, 6])
+    mm = np.empty((3, 5), np.float32)
+    ref.lib().rgref_matmul_f32(ref._fp(np.ascontiguousarray(x)), ref._fp(np.ascontiguousarray(w)), 3, 6, 5,
+                               ref._fp(mm), 0)
+    p = ref.RefProgram(layers, precision=ref.FP32)
+    assert p.num_ops == 2  # Linear (BN folded) and Activation
+    assert_bitexact_f32(p.run(x), np.maximum((mm + b).astype(np.float32), 0))
+
+
+def test_standard_program_affine_and_conv(ref):
+    """A ChannelAffine that does not fold is v * scale + shift per channel on
+    axis 1 (mod.rs:292-306); conv is im2col then W[O, ckk] @ cols plus the
+    bias per channel (kernels.rs:218-265)."""
+    from rustgears_amd.inference import LayerSpec
+    rng = np.random.default_rng(2)
+    sc = rng.standard_normal(3).astype(np.float32)
+    sh = rng.standard_normal(3).astype(np.float32)
+    x = rng.standard_normal((2, 3, 4, 5)).astype(np.float32)
+    p = ref.RefProgram([LayerSpec.ChannelAffine(sc, sh)], precision=ref.FP32)
+    assert_bitexact_f32(p.run(x), (x * sc[None, :, None, None]).astype(np.float32) + sh[None, :, None, None])
+    w = rng.standard_normal((4, 3, 3, 3)).astype(np.float32)
+    bias = rng.standard_normal(4).astype(np.float32)
+    p = ref.RefProgram([LayerSpec.Conv2d(3, 4, 3, 1, 1, w.ravel(), bias)], precision=ref.FP32)
+    y = p.run(x)
+    for i in range(2):
+        cols = np.ascontiguousarray(_im2col_brute(x[i], 3, 4, 5, 3, 1, 1))
+        mm = np.empty((4, 20), np.float32)
+        ref.lib().rgref_matmul_f32(ref._fp(np.ascontiguousarray(w.reshape(4, -1))), ref._fp(cols), 4, 27, 20,
+                                   ref._fp(mm), 0)
+        assert_bitexact_f32(y[i], (mm + bias[:, None]).astype(np.float32).reshape(4, 4, 5))
