@@ -32,8 +32,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "INT8 InferenceSession samples/s; achieved TOPS as % of i8 MFMA peak"
 METRIC_FP16 = "FP16 InferenceSession samples/s; achieved TFLOP/s as % of f16 MFMA peak"
+METRIC_FP32 = "FP32 (ExecutionProvider::Gpu) InferenceSession samples/s; achieved TFLOP/s as % of f32 MFMA peak"
 PEAK_I8_TOPS = 5000.0     # MI355X dense i8 MFMA, 5.0 POP/s
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
+PEAK_F32_TFLOPS = 157.3   # MI355X dense f32 MFMA
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
 
 
@@ -89,10 +91,18 @@ def measured_traffic(workload: str, kernel: str):
     return None
 
 
-def dominant_roofline(name, records, layers, x, workload, fp16=False):
+# per precision: (metric, MFMA peak, dtype, bytes per weight/activation element, oracle precision)
+PRECISIONS = {
+    "int8": (METRIC, PEAK_I8_TOPS, "i8", 1, 0),
+    "fp16": (METRIC_FP16, PEAK_F16_TFLOPS, "f16", 2, 1),
+    "fp32": (METRIC_FP32, PEAK_F32_TFLOPS, "f32", 4, 2),
+}
+
+
+def dominant_roofline(name, records, layers, x, workload, prec="int8"):
     """Roofline of the dominant kernel (largest total kernel time per step)."""
-    peak = PEAK_F16_TFLOPS if fp16 else PEAK_I8_TOPS
-    eb = 2 if fp16 else 1  # bytes per weight / activation element
+    _, peak, _, eb, _ = PRECISIONS[prec]
+    fp16 = prec != "int8"  # HBM traffic was measured for the INT8 kernels only
     best = max(range(len(records)), key=lambda i: records[i].kernel_ns)
     r = records[best]
     if r.kernel_ns <= 0:
@@ -102,7 +112,7 @@ def dominant_roofline(name, records, layers, x, workload, fp16=False):
         # algorithmic bytes of one GEMV launch: weights N*K + f32 bias N +
         # activations B*K (i8, or binary16 for FP16) + f32 output B*N
         lin = [l for l in layers if type(l).__name__ == "Linear"]
-        idx = [i for i, rr in enumerate(records) if "Gemm" in rr.op][: len(lin)]
+        idx = [i for i, rr in enumerate(records) if "Gemm" in rr.op or "Linear" in rr.op][: len(lin)]
         li = lin[idx.index(best)] if best in idx else lin[0]
         b = x.shape[0]
         byts = eb * li.in_features * li.out_features + 4 * li.out_features + eb * b * li.in_features + 4 * b * li.out_features
@@ -124,7 +134,7 @@ def dominant_roofline(name, records, layers, x, workload, fp16=False):
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 
-def cpu_baseline(name, layers, x, target_s: float, fp16=False):
+def cpu_baseline(name, layers, x, target_s: float, prec="int8"):
     """The oracle (C restatement of the reference's rayon INT8 path, or of
     its FP16 path) on a bounded sample of the same workload, all host
     threads: a probe pass over a row sample, then as many passes as fill
@@ -132,7 +142,8 @@ def cpu_baseline(name, layers, x, target_s: float, fp16=False):
     import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
     oracle.set_threads(threads)
-    prog = oracle.RefProgram(layers, precision=oracle.FP16 if fp16 else oracle.INT8)
+    prog = oracle.RefProgram(layers, precision=PRECISIONS[prec][4])
+    fp16 = prec == "fp16"
     n = x.shape[0]
     rows = n if name in ("gemv", "copy") else max(1, min(n, 64))
     t0 = time.perf_counter()
@@ -156,6 +167,11 @@ def cpu_baseline(name, layers, x, target_s: float, fp16=False):
         return {"value": round(passes * rows / dt, 3), "unit": "samples/s", "cores": cores, "kind": "port",
                 "sample": f"{passes} pass(es) over {rows} of {n} samples of the same workload ({dt:.1f} s); FP16 "
                           f"path: Linear serial as in the reference, conv image-parallel"}
+    if prec == "fp32":
+        return {"value": round(passes * rows / dt, 3), "unit": "samples/s", "cores": threads, "kind": "port",
+                "sample": f"{passes} pass(es) over {rows} of {n} samples of the same workload ({dt:.1f} s); the "
+                          f"standard path with a serial-k f32 matmul, row-parallel (the reference's CPU backend "
+                          f"blocks its matmul with AVX2/FMA, cpu.rs:43-160, so this port is slower than it)"}
     return {"value": round(passes * rows / dt, 3), "unit": "samples/s", "cores": threads, "kind": "port",
             "sample": f"{passes} pass(es) over {rows} of {n} samples of the same workload ({dt:.1f} s); row-parallel "
                       f"like rayon (quantize.rs:104), effective parallelism min(rows, threads) = {eff}"}
@@ -173,7 +189,7 @@ def main():
                     help="activation of the linear_stack workload (gelu is the benchmark config)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--precision", default="int8", choices=["int8", "fp16"],
+    ap.add_argument("--precision", default="int8", choices=["int8", "fp16", "fp32"],
                     help="NpuPrecision of the session (the headline metric is INT8)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -186,12 +202,14 @@ def main():
     t_setup = time.perf_counter()
     layers, x, config = build_workload(args.workload, args.batch, args.stack_act)
     fp16 = args.precision == "fp16"
-    provider = rg.ExecutionProvider.mi355x_fp16() if fp16 else rg.ExecutionProvider.mi355x_int8()
+    fp32 = args.precision == "fp32"
+    provider = (rg.ExecutionProvider.mi355x_fp16() if fp16 else
+                rg.ExecutionProvider.Gpu(0) if fp32 else rg.ExecutionProvider.mi355x_int8())
     sess = rg.InferenceSession.from_layers(layers, provider)
     out_shape = sess.output_shape(x.shape)
     dx = rg.DeviceBuffer.from_array(x)
     dy = rg.DeviceBuffer(int(np.prod(out_shape)) * 4)
-    print(f"# setup {time.perf_counter() - t_setup:.1f}s; {sess.compilation_report().splitlines()[1].strip()}",
+    print(f"# setup {time.perf_counter() - t_setup:.1f}s; {sess.compilation_report().splitlines()[-1].strip()}",
           file=sys.stderr, flush=True)
 
     if args.warmup > 0:
@@ -213,19 +231,20 @@ def main():
     value = batch / (ms_per_step / 1e3)
     total_macs = sum(r.macs for r in recs)
     tops = 2 * total_macs / (ms_per_step / 1e3) / 1e12
-    roof, dom = dominant_roofline(args.workload, recs, layers, x, config["workload"], fp16)
+    roof, dom = dominant_roofline(args.workload, recs, layers, x, config["workload"], args.precision)
+    metric, peak, dtype, _, _ = PRECISIONS[args.precision]
     for r in recs:
         print(f"#   {r.op:<44} {r.macs:>14} MACs  op {r.duration_ns / 1e3:9.2f} us  kernel {r.kernel_ns / 1e3:9.2f} us",
               file=sys.stderr)
     line = {
-        "metric": METRIC_FP16 if fp16 else METRIC, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1,
+        "metric": metric, "value": round(value, 2), "unit": "samples/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16" if fp16 else "i8",
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic: RustGears SplitMix64 seeded weights and inputs (rustgears_amd/configs.py)",
         "config": config,
         "tops": round(tops, 2),
-        ("tflops_frac_of_f16_peak" if fp16 else "tops_frac_of_i8_peak"):
-            round(tops / (PEAK_F16_TFLOPS if fp16 else PEAK_I8_TOPS), 4),
+        ("tops_frac_of_i8_peak" if args.precision == "int8" else f"tflops_frac_of_{dtype}_peak"):
+            round(tops / peak, 4),
         "ms_per_step_with_kernel_events": round(dev_ms_ev / args.steps, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": roof,
@@ -241,7 +260,7 @@ def main():
     line["pcie_inclusive"] = {"value": round(batch / host_s, 2), "unit": "samples/s", "ms_per_step": round(host_s * 1e3, 3),
                               "steps": n_host, "note": "host-pointer run(): H2D input + run + D2H output, wall clock"}
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, fp16)
+        line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, args.precision)
     print(json.dumps(line), flush=True)
 
 
