@@ -259,6 +259,18 @@ def main():
     host_s = (time.perf_counter() - h0) / n_host
     line["pcie_inclusive"] = {"value": round(batch / host_s, 2), "unit": "samples/s", "ms_per_step": round(host_s * 1e3, 3),
                               "steps": n_host, "note": "host-pointer run(): H2D input + run + D2H output, wall clock"}
+    # The same from several threads on the one session (run(&self) is Sync):
+    # each call borrows its own worker stream, so copies overlap kernels.
+    threads = 4
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda _: sess.run(x), range(threads)))
+        h0 = time.perf_counter()
+        list(ex.map(lambda _: sess.run(x), range(threads * n_host)))
+        conc_s = time.perf_counter() - h0
+    line["pcie_inclusive_concurrent"] = {
+        "value": round(threads * n_host * batch / conc_s, 2), "unit": "samples/s", "threads": threads,
+        "runs": threads * n_host, "note": "host-pointer run() from several threads on one session, wall clock"}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, args.precision)
     print(json.dumps(line), flush=True)

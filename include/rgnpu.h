@@ -113,7 +113,13 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
  * shape to y_shape / y_ndim.  With y == NULL only the output shape is
  * computed.  Replaces NpuProgram::execute (src/inference/npu.rs:296-421) as
  * called by InferenceSession::run (src/inference/mod.rs:212-221); the
- * profile of the call is kept as last_npu_profile (mod.rs:193-195). */
+ * profile of the call is kept as last_npu_profile (mod.rs:193-195).
+ * Thread-safe like the reference's run(&self) on a Sync session: concurrent
+ * calls on one program each borrow a worker context (own stream and
+ * activation buffers, shared weights; at most 8, further callers wait), so
+ * their copies and kernels overlap and their results do not depend on the
+ * interleaving.  The last call to finish sets the profile.  In capture mode
+ * calls run one at a time on the program's own stream. */
 int rgnpu_program_run(rgnpu_program* prog, const float* x, const int64_t* shape, int32_t ndim,
                       float* y, int64_t y_cap, int64_t* y_shape, int32_t* y_ndim);
 

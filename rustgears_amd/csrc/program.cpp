@@ -18,6 +18,7 @@
 #include <cstring>
 #include <memory>
 #include <array>
+#include <condition_variable>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -161,7 +162,7 @@ struct rgnpu_program {
   hipStream_t stream = nullptr;
   int64_t original_layers = 0;
   int64_t fp32_bytes = 0, npu_bytes = 0;
-  std::vector<std::unique_ptr<Op>> ops;
+  std::vector<std::shared_ptr<Op>> ops;  // device weights; shared with the workers
   std::unique_ptr<Plan> plan;
   int profiling = 1;
   bool capture = false;
@@ -172,7 +173,20 @@ struct rgnpu_program {
   rgnpu_profile prof{};
   std::vector<rgnpu_op_record> records;
   std::mutex mu;
+  // Concurrent host runs (InferenceSession::run takes &self and is Sync,
+  // mod.rs:146-151, 212-221): each call borrows a worker -- the same ops
+  // (weights), its own stream, plans and events -- so calls on one handle
+  // run side by side on the device, their copies overlapping other calls'
+  // kernels.  The handle's own stream serves run_device, benchmark and
+  // capture.
+  std::mutex pool_mu;
+  std::condition_variable pool_cv;
+  std::vector<std::unique_ptr<rgnpu_program>> workers;
+  std::vector<char> worker_busy;
 };
+
+// Upper bound on workers (concurrent host runs) per handle.
+static constexpr size_t kMaxWorkers = 8;
 
 namespace rgnpu {
 
@@ -1129,6 +1143,10 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
 
 void rgnpu_program_destroy(rgnpu_program* P) {
   if (!P) return;
+  for (auto& w : P->workers) {
+    rgnpu_program* W = w.release();
+    rgnpu_program_destroy(W);
+  }
   (void)hipSetDevice(P->device);
   if (P->stream) (void)hipStreamSynchronize(P->stream);
   P->plan.reset();
@@ -1138,15 +1156,19 @@ void rgnpu_program_destroy(rgnpu_program* P) {
   delete P;
 }
 
-int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, int32_t ndim, float* y, int64_t y_cap,
-                      int64_t* y_shape, int32_t* y_ndim) {
-  RG_API_BEGIN
-  if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+}  // extern "C"
+
+namespace rgnpu {
+
+// One host-pointer run on P's own stream and plan (P is the handle or one of
+// its workers).
+static void run_host(rgnpu_program* P, const float* x, const int64_t* shape, int32_t ndim, float* y, int64_t y_cap,
+                     int64_t* y_shape, int32_t* y_ndim) {
   std::lock_guard<std::mutex> lk(P->mu);
   RG_HIP(hipSetDevice(P->device));
   Plan& plan = get_plan(P, shape, ndim);
   write_shape(plan, y_shape, y_ndim);
-  if (!y) return RGNPU_OK;
+  if (!y) return;
   if (!x && plan.in_len > 0) throw Error(RGNPU_ERR_INVALID, "x is NULL");
   if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
   plan.host_in.ensure((size_t)plan.in_len * sizeof(float));
@@ -1158,6 +1180,77 @@ int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, in
     RG_HIP(hipMemcpyAsync(y, plan.host_out.p, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToHost, P->stream));
   RG_HIP(hipStreamSynchronize(P->stream));
   finalize_profile(P);
+}
+
+static rgnpu_program* acquire_worker(rgnpu_program* P) {
+  std::unique_lock<std::mutex> lk(P->pool_mu);
+  for (;;) {
+    for (size_t i = 0; i < P->workers.size(); i++)
+      if (!P->worker_busy[i]) {
+        P->worker_busy[i] = 1;
+        return P->workers[i].get();
+      }
+    if (P->workers.size() < kMaxWorkers) {
+      auto W = std::make_unique<rgnpu_program>();
+      W->device = P->device;
+      W->precision = P->precision;
+      W->original_layers = P->original_layers;
+      W->fp32_bytes = P->fp32_bytes;
+      W->npu_bytes = P->npu_bytes;
+      W->ops = P->ops;
+      RG_HIP(hipSetDevice(P->device));
+      RG_HIP(hipStreamCreateWithFlags(&W->stream, hipStreamNonBlocking));
+      P->workers.push_back(std::move(W));
+      P->worker_busy.push_back(1);
+      return P->workers.back().get();
+    }
+    P->pool_cv.wait(lk);
+  }
+}
+
+static void release_worker(rgnpu_program* P, rgnpu_program* W) {
+  {
+    std::lock_guard<std::mutex> lk(P->pool_mu);
+    for (size_t i = 0; i < P->workers.size(); i++)
+      if (P->workers[i].get() == W) P->worker_busy[i] = 0;
+  }
+  P->pool_cv.notify_one();
+}
+
+}  // namespace rgnpu
+
+extern "C" {
+
+int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, int32_t ndim, float* y, int64_t y_cap,
+                      int64_t* y_shape, int32_t* y_ndim) {
+  RG_API_BEGIN
+  if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+  bool capture;
+  int profiling;
+  {
+    std::lock_guard<std::mutex> lk(P->mu);
+    capture = P->capture;
+    profiling = P->profiling;
+  }
+  if (capture) {
+    // capture taps live on the handle's own plan
+    run_host(P, x, shape, ndim, y, y_cap, y_shape, y_ndim);
+    return RGNPU_OK;
+  }
+  rgnpu_program* W = acquire_worker(P);
+  struct Release {
+    rgnpu_program *P, *W;
+    ~Release() { release_worker(P, W); }
+  } rel{P, W};
+  W->profiling = profiling;
+  run_host(W, x, shape, ndim, y, y_cap, y_shape, y_ndim);
+  if (y && W->have_profile) {
+    // the last completed run's profile (mod.rs:217)
+    std::lock_guard<std::mutex> lk(P->mu);
+    P->prof = W->prof;
+    P->records = W->records;
+    P->have_profile = true;
+  }
   RG_API_END
 }
 

@@ -1,0 +1,62 @@
+"""Concurrent InferenceSession.run on one session (run(&self) is Sync,
+mod.rs:146-151, 212-221): host-pointer runs from several threads borrow
+separate workers (own stream, plans, absmax slots) that share the device
+weights.  Every concurrent result must equal the serial one bit for bit,
+whatever the interleaving, and the profile stays a complete profile."""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("prec", ["int8", "fp16", "fp32"])
+def test_concurrent_runs_match_serial(rg, ref, prec):
+    from rustgears_amd import configs
+    model, _ = configs.deep_mlp(rows=384)
+    provider = {"int8": rg.ExecutionProvider.mi355x_int8(), "fp16": rg.ExecutionProvider.mi355x_fp16(),
+                "fp32": rg.ExecutionProvider.Gpu(0)}[prec]
+    layers = model.export()
+    sess = rg.InferenceSession.from_layers(layers, provider)
+    # different magnitudes and row counts: a shared slot or buffer between
+    # concurrent runs would change scales or shapes
+    inputs = [(rg.randn([384 if i % 3 else 200, 784]) * (0.1 + i)).astype(np.float32) for i in range(8)]
+    want = [sess.run(x) for x in inputs]
+    print(f"[concurrency] {prec}: 6 threads x {3 * len(inputs)} runs", flush=True)
+    with ThreadPoolExecutor(6) as ex:
+        got = list(ex.map(sess.run, inputs * 3))
+    for i, (g, w) in enumerate(zip(got, want * 3)):
+        assert_bitexact_f32(g, w, f"{prec} run {i}")
+    if prec == "int8":
+        assert_bitexact_f32(want[0], ref.RefProgram(layers).run(inputs[0]), "int8 vs oracle")
+        prof = sess.last_npu_profile()
+        assert prof is not None and prof.fused_ops == 3 and len(prof.records) == 3
+    sess.close()
+
+
+def test_concurrent_runs_with_device_runs_and_capture(rg, ref):
+    """Host runs on workers while the handle's own stream serves
+    run_device; capture mode runs on the handle and stays exact."""
+    from rustgears_amd import configs
+    model, x = configs.deep_mlp(rows=256)
+    layers = model.export()
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    want = sess.run(x)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(want.nbytes)
+    with ThreadPoolExecutor(4) as ex:
+        futs = [ex.submit(sess.run, x) for _ in range(8)]
+        for _ in range(4):
+            sess.run_device(dx, x.shape, dy)
+        sess.synchronize()
+        for f in futs:
+            assert_bitexact_f32(f.result(), want, "host run beside run_device")
+    assert_bitexact_f32(dy.download(want.shape), want, "run_device")
+    sess.set_capture(True)
+    y = sess.run(x)
+    assert_bitexact_f32(y, want, "capture run")
+    assert_bitexact_f32(sess.capture(2, 3).reshape(want.shape), want, "capture tap")
+    sess.close()
