@@ -623,17 +623,30 @@ int64_t rgref_program_op_label(const rgref_program* p, int64_t i, char* buf, int
  * orders it (wgpu_impl.rs:20-48): per output a serial f32 sum over k in
  * order, multiply then add.  (The CPU backend's AVX2/FMA blocking,
  * cpu.rs:43-160, orders the same products differently.) */
+/* c[r, j] = fl(... fl(fl(0 + fl(a[r,0] b[0,j])) + fl(a[r,1] b[1,j])) ...): each
+   output sums its products serially in increasing p.  The loop keeps one
+   accumulator per output column of a block and walks b along its rows, so
+   the work is spread over (row, column block) pairs and b is read with unit
+   stride; every accumulator still adds its products in the same order. */
+#define RGREF_MM_JB 256
 void rgref_matmul_f32(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c, int parallel) {
-#pragma omp parallel for schedule(dynamic, 4) num_threads(rgref_get_threads()) if (parallel && m * k * n >= 32 * 1024)
-  for (int64_t r = 0; r < m; r++)
-    for (int64_t j = 0; j < n; j++) {
-      float acc = 0.0f;
-      for (int64_t p = 0; p < k; p++) {
-        float prod = a[r * k + p] * b[p * n + j];
-        acc = acc + prod;
+  const int64_t nb = (n + RGREF_MM_JB - 1) / RGREF_MM_JB;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(rgref_get_threads()) if (parallel && m * k * n >= 32 * 1024)
+  for (int64_t t = 0; t < m * nb; t++) {
+    const int64_t r = t / nb, j0 = (t % nb) * RGREF_MM_JB;
+    const int64_t w = n - j0 < RGREF_MM_JB ? n - j0 : RGREF_MM_JB;
+    float acc[RGREF_MM_JB];
+    for (int64_t j = 0; j < w; j++) acc[j] = 0.0f;
+    for (int64_t p = 0; p < k; p++) {
+      const float av = a[r * k + p];
+      const float* br = b + p * n + j0;
+      for (int64_t j = 0; j < w; j++) {
+        const float prod = av * br[j];
+        acc[j] = acc[j] + prod;
       }
-      c[r * n + j] = acc;
     }
+    for (int64_t j = 0; j < w; j++) c[r * n + j0 + j] = acc[j];
+  }
 }
 
 static int standard_layer(ref_op* op, float** pdata, int64_t* plen, int64_t* shape, int* pnd, int parallel) {

@@ -26,6 +26,7 @@
 
 #include "../../include/rgnpu.h"
 #include "devmath.h"
+#include "hostcopy.h"
 #include "rgnpu_internal.h"
 
 namespace rgnpu {
@@ -183,6 +184,7 @@ struct rgnpu_program {
   std::condition_variable pool_cv;
   std::vector<std::unique_ptr<rgnpu_program>> workers;
   std::vector<char> worker_busy;
+  rgnpu::Staging staging;  // pinned ring for this stream's host copies
 };
 
 // Upper bound on workers (concurrent host runs) per handle.
@@ -1173,11 +1175,17 @@ static void run_host(rgnpu_program* P, const float* x, const int64_t* shape, int
   if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
   plan.host_in.ensure((size_t)plan.in_len * sizeof(float));
   plan.host_out.ensure((size_t)plan.out_len * sizeof(float));
+  // On any exit the stream drains, so no DMA still reads or writes the
+  // staging ring (or the caller's buffers) once this call has returned.
+  struct Drain {
+    hipStream_t s;
+    ~Drain() { (void)hipStreamSynchronize(s); }
+  } drain{P->stream};
   if (plan.in_len > 0)
-    RG_HIP(hipMemcpyAsync(plan.host_in.p, x, (size_t)plan.in_len * sizeof(float), hipMemcpyHostToDevice, P->stream));
+    RG_HIP(copy_to_device(P->staging, plan.host_in.p, x, (size_t)plan.in_len * sizeof(float), P->stream));
   enqueue_profiled(P, plan, plan.host_in.as<float>(), plan.host_out.as<float>());
   if (plan.out_len > 0)
-    RG_HIP(hipMemcpyAsync(y, plan.host_out.p, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToHost, P->stream));
+    RG_HIP(copy_to_host(P->staging, y, plan.host_out.p, (size_t)plan.out_len * sizeof(float), P->stream));
   RG_HIP(hipStreamSynchronize(P->stream));
   finalize_profile(P);
 }

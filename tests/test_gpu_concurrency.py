@@ -60,3 +60,56 @@ def test_concurrent_runs_with_device_runs_and_capture(rg, ref):
     assert_bitexact_f32(y, want, "capture run")
     assert_bitexact_f32(sess.capture(2, 3).reshape(want.shape), want, "capture tap")
     sess.close()
+
+
+@pytest.mark.parametrize("rows", [255, 256, 1023, 2049, 10000])
+def test_staged_host_copies(rg, ref, rows):
+    """run() moves inputs and outputs of 1 MiB and more through the pinned
+    staging ring, in chunks of a quarter of the copy between 1 and 8 MiB:
+    255 rows x 1024 f32 stays below 1 MiB (plain copy), 256 rows is one
+    1 MiB chunk, 1023 and 2049 rows end in a ragged chunk, and 10000 rows
+    (8 MiB chunks) needs more chunks than the ring's 4 slots.  The result
+    equals the device-resident run bit for bit."""
+    from rustgears_amd import configs
+    model, _ = configs.linear_stack(rows=rows, width=1024, depth=2)
+    layers = model.export()
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    x = (rg.randn([rows, 1024]) * 3.0).astype(np.float32)
+    print(f"[staging] rows={rows} in={x.nbytes} bytes", flush=True)
+    y = sess.run(x)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(y.nbytes)
+    sess.run_device(dx, x.shape, dy)
+    sess.synchronize()
+    assert_bitexact_f32(y, dy.download(y.shape), f"host vs device run, rows {rows}")
+    assert_bitexact_f32(sess.run(x), y, "second host run")
+    if rows == 2049:
+        assert_bitexact_f32(y, ref.RefProgram(layers).run(x), "staged run vs oracle")
+    sess.close()
+
+
+def test_staged_input_small_output_and_concurrency(rg):
+    """A staged input with an output below the staging size, then several
+    threads each moving ~40 MB each way on their own worker ring."""
+    from rustgears_amd import configs
+    model, _ = configs.deep_mlp(rows=6000, d_in=1024, hidden=1024, d_out=10)
+    sess = rg.InferenceSession.from_layers(model.export(), rg.ExecutionProvider.mi355x_int8())
+    x = rg.uniform([6000, 1024], 0.0, 1.0).astype(np.float32)
+    y = sess.run(x)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(y.nbytes)
+    sess.run_device(dx, x.shape, dy)
+    sess.synchronize()
+    assert_bitexact_f32(y, dy.download(y.shape), "staged input, small output")
+    sess.close()
+
+    model, _ = configs.linear_stack(rows=10000, width=1024, depth=1)
+    sess = rg.InferenceSession.from_layers(model.export(), rg.ExecutionProvider.mi355x_int8())
+    xs = [(rg.randn([10000, 1024]) * (1 + i)).astype(np.float32) for i in range(4)]
+    want = [sess.run(x) for x in xs]
+    print("[staging] 4 threads x 12 runs of 41 MB", flush=True)
+    with ThreadPoolExecutor(4) as ex:
+        got = list(ex.map(sess.run, xs * 3))
+    for i, (g, w) in enumerate(zip(got, want * 3)):
+        assert_bitexact_f32(g, w, f"concurrent staged run {i}")
+    sess.close()

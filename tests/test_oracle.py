@@ -523,6 +523,23 @@ def test_standard_matmul_serial_order(ref, m, k, n):
     assert_bitexact_f32(c, want)
 
 
+@pytest.mark.parametrize("m,k,n,par", [(2, 9, 600, 0), (1, 40, 257, 1), (5, 33, 513, 1), (64, 3, 1, 1)])
+def test_standard_matmul_column_blocks(ref, m, k, n, par):
+    """The same serial order across several (and ragged) column blocks, with
+    and without the parallel split: numpy's elementwise float32 products and
+    sums, accumulated over k in order."""
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    c = np.empty((m, n), np.float32)
+    ref.lib().rgref_matmul_f32(ref._fp(a), ref._fp(b), m, k, n, ref._fp(c), par)
+    acc = np.zeros((m, n), np.float32)
+    for p in range(k):
+        acc = acc + (a[:, p:p + 1] * b[p:p + 1, :])
+    assert acc.dtype == np.float32
+    assert_bitexact_f32(c, acc)
+
+
 def test_standard_program_linear_bn_relu(ref, rg):
     """Standard program: BN folded like the NPU compile (mod.rs:168-171), then
     matmul with the exported [in, out] weights, the bias added separately,
