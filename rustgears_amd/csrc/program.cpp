@@ -1422,17 +1422,21 @@ int rgnpu_program_set_capture(rgnpu_program* P, int32_t on) {
 
 int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* dst, int64_t cap_bytes) {
   try {
-    if (!P || !P->plan || !P->capture_valid || i < 0 || i >= (int64_t)P->ops.size()) {
+    if (!P) {
       rgnpu::g_last_error = "no capture available";
       return -1;
     }
     std::lock_guard<std::mutex> lk(P->mu);
+    if (!P->plan || !P->capture_valid || i < 0 || i >= (int64_t)P->ops.size()) {
+      rgnpu::g_last_error = "no capture available";
+      return -1;
+    }
     RG_HIP(hipSetDevice(P->device));
     RG_HIP(hipStreamSynchronize(P->stream));
     Plan& plan = *P->plan;
     const Op& op = *P->ops[(size_t)i];
     const OpPlan& pl = plan.ops[(size_t)i];
-    // FP16 has no quantized activations, scales or integer sums to expose.
+    // FP16 and FP32 have no quantized activations, scales or integer sums to expose.
     const bool gemm = (op.kind == OP_LINEAR || op.kind == OP_CONV) && P->precision == RGNPU_PRECISION_INT8;
     auto copy_out = [&](const void* src, int64_t count, size_t elem) -> int64_t {
       if (dst) {
