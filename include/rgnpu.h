@@ -134,15 +134,22 @@ int rgnpu_program_synchronize(rgnpu_program* prog);
 
 /* Throughput measurement on device buffers: enqueues `iters` runs back to
  * back on the program's stream, bracketed by two HIP events, waits, and
- * returns the elapsed device time.  Without per_kernel_events the runs record
- * no events of their own.  With it, each run also records a start and an end
- * marker, every kernel of every run records the completion timestamp of its
- * own dispatch (no marker packet per kernel), and avg[i] receives op i's mean
- * op time (ns, from the previous kernel's completion to its last kernel's)
- * and main-kernel time (kernel_ns) over the iterations.  No counterpart in
- * the reference; this is the bench harness's timed region. */
+ * returns the elapsed device time.  `flags`:
+ *  - 0: the runs record no events of their own;
+ *  - RGNPU_BENCH_KERNEL_EVENTS: each run also records a start and an end
+ *    marker, every kernel of every run records the completion timestamp of
+ *    its own dispatch (no marker packet per kernel), and avg[i] receives op
+ *    i's mean op time (ns, from the previous kernel's completion to its last
+ *    kernel's) and main-kernel time (kernel_ns) over the iterations;
+ *  - RGNPU_BENCH_EVICT_CACHE (with or without the above): before each run a
+ *    kernel reads 512 MiB of a zero buffer, so the run finds none of its own
+ *    data in the 256 MB memory-side cache.  That read is outside every op
+ *    interval but inside total_ms.
+ * No counterpart in the reference; this is the bench harness's timed region. */
+#define RGNPU_BENCH_KERNEL_EVENTS 1
+#define RGNPU_BENCH_EVICT_CACHE 2
 int rgnpu_program_benchmark(rgnpu_program* prog, const float* d_x, const int64_t* shape, int32_t ndim, float* d_y,
-                            int64_t y_cap, int32_t iters, int32_t per_kernel_events, double* total_ms,
+                            int64_t y_cap, int32_t iters, int32_t flags, double* total_ms,
                             rgnpu_op_record* avg, int32_t cap);
 
 /* Profiling level: 0 = total time only, 1 = per-op and per-kernel HIP events.

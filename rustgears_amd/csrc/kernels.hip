@@ -138,6 +138,26 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {
   RG_LAUNCH(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
 }
 
+// Reads n 16-byte words so that the memory-side cache (256 MB on MI355X)
+// holds them instead of whatever a run left there.  The xor of everything
+// read lands in sink[0] only if it equals `never`, which the caller picks
+// so that the reads cannot be dropped (the buffer is zero, `never` is not).
+__global__ __launch_bounds__(256) void evict_kernel(const v4i* __restrict__ p, int64_t n, uint32_t never,
+                                                    uint32_t* __restrict__ sink) {
+  uint32_t x = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const v4i v = p[i];  // plain loads: they allocate in the memory-side cache
+    x ^= (uint32_t)(v[0] ^ v[1] ^ v[2] ^ v[3]);
+  }
+  if (x == never) sink[0] = x;
+}
+
+void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s) {
+  const int64_t n = bytes / 16;
+  if (n <= 0) return;
+  RG_LAUNCH(evict_kernel, dim3(4096), dim3(256), 0, s, reinterpret_cast<const v4i*>(p), n, 0x9e3779b9u, sink);
+}
+
 // ---------------------------------------------------------------------------
 // absmax: QuantTensor::from_f32's `fold(0, max(|v|))` (quantize.rs:19) as a
 // grid reduction.  Non-negative f32 order equals u32 bit order, so a u32

@@ -185,7 +185,11 @@ struct rgnpu_program {
   std::vector<std::unique_ptr<rgnpu_program>> workers;
   std::vector<char> worker_busy;
   rgnpu::Staging staging;  // pinned ring for this stream's host copies
+  DevBuf evict;            // zero buffer read between benchmark runs on request
 };
+
+// Bytes read between benchmark runs to displace the 256 MB memory-side cache.
+static constexpr int64_t kEvictBytes = int64_t(512) << 20;
 
 // Upper bound on workers (concurrent host runs) per handle.
 static constexpr size_t kMaxWorkers = 8;
@@ -1278,10 +1282,11 @@ int rgnpu_program_run_device(rgnpu_program* P, const float* d_x, const int64_t* 
 }
 
 int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* shape, int32_t ndim, float* d_y,
-                            int64_t y_cap, int32_t iters, int32_t per_kernel_events, double* total_ms,
+                            int64_t y_cap, int32_t iters, int32_t flags, double* total_ms,
                             rgnpu_op_record* avg, int32_t cap) {
   RG_API_BEGIN
   if (!P || !shape || !d_y || iters <= 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
+  const bool per_kernel_events = (flags & RGNPU_BENCH_KERNEL_EVENTS) != 0;
   std::lock_guard<std::mutex> lk(P->mu);
   RG_HIP(hipSetDevice(P->device));
   Plan& plan = get_plan(P, shape, ndim);
@@ -1303,11 +1308,20 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
       create_run_event(&evs[i], i % (size_t)per);
   }
   hipEvent_t t0 = evs[per * sets], t1 = evs[per * sets + 1];
+  const bool evict = (flags & RGNPU_BENCH_EVICT_CACHE) != 0;
+  if (evict && !P->evict.p) {
+    P->evict.ensure(kEvictBytes + 256);
+    launch_fill_u32(P->evict.as<uint32_t>(), (kEvictBytes + 256) / 4, 0u, P->stream);
+  }
   RG_HIP(hipStreamSynchronize(P->stream));
   RG_HIP(hipEventRecord(t0, P->stream));
   for (int32_t it = 0; it < iters; it++) {
     hipEvent_t* set = per_kernel_events ? evs.data() + per * (size_t)it : nullptr;
-    enqueue(P, plan, d_x, d_y, set, per_kernel_events != 0);
+    // before the run's start marker: no op interval includes it
+    if (evict)
+      launch_evict(P->evict.p, kEvictBytes,
+                   reinterpret_cast<uint32_t*>(static_cast<char*>(P->evict.p) + kEvictBytes), P->stream);
+    enqueue(P, plan, d_x, d_y, set, per_kernel_events);
   }
   RG_HIP(hipEventRecord(t1, P->stream));
   RG_HIP(hipEventSynchronize(t1));

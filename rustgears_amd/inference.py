@@ -445,13 +445,17 @@ class InferenceSession:
                                                  shp, ctypes.byref(nd)))
         return tuple(shp[i] for i in range(nd.value))
 
-    def benchmark(self, d_x: DeviceBuffer, shape, d_y: DeviceBuffer, iters: int, per_kernel_events: bool = True):
-        """rgnpu_program_benchmark: (total device ms, [OpRecord averages])."""
+    def benchmark(self, d_x: DeviceBuffer, shape, d_y: DeviceBuffer, iters: int, per_kernel_events: bool = True,
+                  evict_cache: bool = False):
+        """rgnpu_program_benchmark: (total device ms, [OpRecord averages]).
+        evict_cache: read 512 MiB of other data before each run, so that no run
+        finds its weights in the 256 MB memory-side cache."""
         sh = (ctypes.c_int64 * len(shape))(*shape)
         ms = ctypes.c_double()
         recs = (N.COpRecord * 256)()
+        flags = (1 if per_kernel_events else 0) | (2 if evict_cache else 0)
         N.check(N.lib().rgnpu_program_benchmark(self._h, d_x.ptr, sh, len(shape), d_y.ptr, d_y.nbytes // 4,
-                                                int(iters), 1 if per_kernel_events else 0, ctypes.byref(ms),
+                                                int(iters), flags, ctypes.byref(ms),
                                                 ctypes.cast(recs, ctypes.c_void_p), 256))
         n = N.lib().rgnpu_program_num_ops(self._h)
         return ms.value, [OpRecord(recs[i].op.decode(), int(recs[i].macs), int(recs[i].ns), int(recs[i].kernel_ns))

@@ -254,6 +254,28 @@ def test_device_resident_run_matches_host_run(rg, ref):
     assert sess.last_npu_profile().total_time_ns > 0
 
 
+def test_benchmark_regions(rg, ref):
+    """The bench's timed regions (plain, with kernel events, with the
+    memory-side cache displaced before each run) compute the same output as
+    run(), and the event regions time every op."""
+    from rustgears_amd import configs
+    model, x = configs.deep_mlp(rows=512)
+    sess = make_session(rg, model.export())
+    want = sess.run(x)
+    dx = rg.DeviceBuffer.from_array(x)
+    dy = rg.DeviceBuffer(want.nbytes)
+    for kw in ({"per_kernel_events": False}, {"per_kernel_events": True},
+               {"per_kernel_events": True, "evict_cache": True}, {"per_kernel_events": False, "evict_cache": True}):
+        print(f"[benchmark] {kw}", flush=True)
+        ms, recs = sess.benchmark(dx, x.shape, dy, 3, **kw)
+        assert ms > 0
+        assert_bitexact_f32(dy.download(want.shape), want, str(kw))
+        assert len(recs) == 3 and [r.op for r in recs] == [r.op for r in sess.last_npu_profile().records]
+        if kw["per_kernel_events"]:
+            assert all(r.duration_ns > 0 and r.kernel_ns > 0 for r in recs)
+        dy.upload(np.zeros(want.shape, np.float32))
+
+
 @pytest.mark.parametrize("kind", ["linear_small", "linear_large", "conv_first", "pool_first"])
 def test_consecutive_runs_on_one_session(rg, ref, kind):
     """Several runs of one session with alternating input magnitudes: the
