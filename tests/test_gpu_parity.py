@@ -124,6 +124,16 @@ def test_gemv_silu_full(rg, ref, batch):
     check_against_oracle(rg, ref, layers, x, f"gemv full b{batch}")
 
 
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_gemv_relu_full(rg, ref, batch):
+    """The ReLU twin of the decode-shape config, a model the reference itself
+    can express (SiLU is the build's extension)."""
+    from rustgears_amd import configs
+    from rustgears_amd.inference import Activation
+    layers, x = configs.gemv(batch=batch, act=Activation.RELU)
+    check_against_oracle(rg, ref, layers, x, f"gemv relu full b{batch}")
+
+
 @pytest.mark.parametrize("batch", [1, 8])
 def test_gemv_silu_scaled(rg, ref, batch):
     from rustgears_amd import configs
