@@ -1690,12 +1690,87 @@ __global__ __launch_bounds__(256) void maxpool_kernel(const float* __restrict__ 
   }
 }
 
+// The 2 x 2, stride 2 window on rows of a multiple of 4 floats: a thread
+// takes pairs of neighbouring outputs, two 16-byte loads (one per window
+// row) each, all issued before any is used.  A block of 1024 threads covers
+// up to 4096 pairs of one image (a whole image of the CNN's first pool), so
+// a per-image absmax costs one device-scope atomic per block: many blocks
+// raising neighbouring slots serialise at the memory side.  Each output takes
+// its window in the reference's order (0,0), (0,1), (1,0), (1,1) with the
+// same rule as maxpool_kernel, so ties and NaNs resolve alike.
+__device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
+
+constexpr int kPool2Threads = 1024, kPool2PerThread = 4;
+
+__global__ __launch_bounds__(kPool2Threads) void maxpool2_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                 uint32_t C, uint32_t H, uint32_t W, uint32_t OH,
+                                                                 uint32_t OW, uint32_t pairs, uint32_t* absmax_out,
+                                                                 int per_image) {
+  const int64_t b = blockIdx.y;
+  const uint32_t half = OW >> 1, plane = OH * half;
+  uint32_t amax = 0;
+  float4 u[kPool2PerThread], v[kPool2PerThread];
+  int64_t yo[kPool2PerThread];
+  bool ok[kPool2PerThread];
+#pragma unroll
+  for (int i = 0; i < kPool2PerThread; i++) {
+    const uint32_t p = (blockIdx.x * kPool2PerThread + i) * kPool2Threads + threadIdx.x;
+    ok[i] = p < pairs;
+    const uint32_t q = ok[i] ? p : 0u;
+    const uint32_t c = q / plane, r = q - c * plane;
+    const uint32_t oy = r / half, ox = (r - oy * half) * 2;
+    const float* row0 = x + ((b * C + c) * (int64_t)H + 2 * oy) * (int64_t)W + 2 * ox;
+    if (ok[i]) {
+      u[i] = *reinterpret_cast<const float4*>(row0);
+      v[i] = *reinterpret_cast<const float4*>(row0 + W);
+    }
+    yo[i] = b * (int64_t)pairs * 2 + (int64_t)c * OH * OW + (int64_t)oy * OW + ox;
+  }
+#pragma unroll
+  for (int i = 0; i < kPool2PerThread; i++) {
+    if (!ok[i]) continue;
+    float o0 = -__builtin_inff(), o1 = -__builtin_inff();
+    o0 = pool_take(o0, u[i].x); o0 = pool_take(o0, u[i].y); o0 = pool_take(o0, v[i].x); o0 = pool_take(o0, v[i].y);
+    o1 = pool_take(o1, u[i].z); o1 = pool_take(o1, u[i].w); o1 = pool_take(o1, v[i].z); o1 = pool_take(o1, v[i].w);
+    *reinterpret_cast<float2*>(y + yo[i]) = make_float2(o0, o1);
+    const uint32_t k0 = rgmath::absmax_key(o0), k1 = rgmath::absmax_key(o1);
+    const uint32_t k = k0 > k1 ? k0 : k1;
+    amax = k > amax ? k : amax;
+  }
+  if (absmax_out) {
+    __shared__ uint32_t red[kPool2Threads / 64];
+    amax = wave_max_u32(amax);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t m = lane < kPool2Threads / 64 ? red[lane] : 0u;
+      m = wave_max_u32(m);
+      if (lane == 0) {
+        if (per_image) {
+          if (m) atomicMax(absmax_out + b, m);
+        } else {
+          spread_max(absmax_out, m);
+        }
+      }
+    }
+  }
+}
+
 void launch_maxpool(const float* x, float* y, int64_t n, int64_t C, int64_t H, int64_t W, int64_t k, int64_t stride,
                     int64_t OH, int64_t OW, uint32_t* absmax_out, int absmax_per_image, hipStream_t s) {
   const int64_t per = C * OH * OW;
   if (per <= 0 || n <= 0) return;
   if (C * H * W >= ((int64_t)1 << 32) || n > 65535)
     throw std::logic_error("max pool: image or batch too large for the 32-bit kernel indexing");
+  if (k == 2 && stride == 2 && W % 4 == 0 && OW * 2 == W && OH * 2 <= H &&
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0) {
+    const int64_t pairs = per / 2, per_block = (int64_t)kPool2Threads * kPool2PerThread;
+    RG_LAUNCH(maxpool2_kernel, dim3((unsigned)((pairs + per_block - 1) / per_block), (unsigned)n), dim3(kPool2Threads), 0, s, x, y,
+              (uint32_t)C, (uint32_t)H, (uint32_t)W, (uint32_t)OH, (uint32_t)OW, (uint32_t)pairs, absmax_out,
+              absmax_per_image);
+    return;
+  }
   // about 16 outputs per thread, at most 64 blocks per image
   int64_t bx = (per + 256 * 16 - 1) / (256 * 16);
   if (bx > 64) bx = 64;
