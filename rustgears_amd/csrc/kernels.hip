@@ -1307,6 +1307,86 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
   }
 }
 
+// INT8 Linear with at most 16 outputs per row (the classifier heads: D's
+// 1024 -> 10, C's 256 -> 10, Q's 32 -> 3).  A 128 x 128 MFMA tile would waste
+// most of its columns, so a wave takes one row at a time instead: lane l
+// holds 16 bytes of every 1 KiB K chunk of the row and of the N weight rows
+// (those are a few KiB and stay in L1), sums them with sdot4, and the wave's
+// N sums are reduce-scattered as in gemv_kernel before the fused epilogue
+// (quantize.rs:109-111; integer sums are exact in any order).
+template <int NN>
+__global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                          int64_t M, int64_t N, int64_t Kpad, Epilogue ep) {
+  constexpr int S = pow2_at_least(NN);
+  constexpr int SPREAD = 64 / S;
+  const int lane = threadIdx.x & 63;
+  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  const int sidx = lane / SPREAD;
+  const bool owner = (lane % SPREAD) == 0 && sidx < N;
+  const float bias_v = ep.bias[sidx < N ? sidx : N - 1];
+  const int64_t ntrip = (Kpad + 1023) / 1024;
+  const int64_t klast = Kpad - 16;
+  uint32_t amax = 0;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < M; row += (int64_t)gridDim.x * 4) {
+    int32_t acc[S];
+#pragma unroll
+    for (int i = 0; i < S; i++) acc[i] = 0;
+    for (int64_t t = 0; t < ntrip; t++) {
+      const int64_t k = t * 1024 + lane * 16;
+      const bool ok = k < Kpad;
+      const int64_t kk = ok ? k : klast;
+      const v4i al = *reinterpret_cast<const v4i*>(A + row * Kpad + kk);
+      const v4i av = ok ? al : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int n = 0; n < NN; n++) {
+        const v4i w = *reinterpret_cast<const v4i*>(B + (int64_t)n * Kpad + kk);
+        int32_t c = acc[n];
+        c = __builtin_amdgcn_sdot4(av[0], w[0], c, false);
+        c = __builtin_amdgcn_sdot4(av[1], w[1], c, false);
+        c = __builtin_amdgcn_sdot4(av[2], w[2], c, false);
+        c = __builtin_amdgcn_sdot4(av[3], w[3], c, false);
+        acc[n] = c;
+      }
+    }
+    const int32_t mine = wave_reduce_scatter<S, false>(acc, lane);
+    const float prod = (float)mine * cs;
+    const float pre = prod + bias_v;
+    if (owner) {
+      float v;
+      switch (ep.act) {
+        case rgmath::ACT_RELU: v = act_fixed<rgmath::ACT_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SIGMOID: v = act_fixed<rgmath::ACT_SIGMOID>(pre, ep.act_param); break;
+        case rgmath::ACT_TANH: v = act_fixed<rgmath::ACT_TANH>(pre, ep.act_param); break;
+        case rgmath::ACT_GELU: v = act_fixed<rgmath::ACT_GELU>(pre, ep.act_param); break;
+        case rgmath::ACT_LEAKY_RELU: v = act_fixed<rgmath::ACT_LEAKY_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SILU: v = act_fixed<rgmath::ACT_SILU>(pre, ep.act_param); break;
+        default: v = pre; break;
+      }
+      ep.y[row * N + sidx] = v;
+      if (ep.acc_out) ep.acc_out[row * N + sidx] = mine;
+      const uint32_t key = rgmath::absmax_key(v);
+      amax = key > amax ? key : amax;
+    }
+  }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
+  }
+}
+
+void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
+                        hipStream_t s) {
+  if (N <= 0 || N > kNarrowMaxN || Kpad % 16 || Kpad <= 0) throw std::logic_error("narrow GEMM: N must be 1..16");
+  if (M <= 0) return;
+  const int64_t blocks = std::min<int64_t>((M + 3) / 4, 8192);
+  if (N <= 4)
+    RG_LAUNCH(gemm_narrow_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+  else if (N <= 8)
+    RG_LAUNCH(gemm_narrow_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+  else
+    RG_LAUNCH(gemm_narrow_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+}
+
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
   launch_gemv_any<kModeI8>(A, B, M, N, Npad, Kpad, ep, s);

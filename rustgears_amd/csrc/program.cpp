@@ -727,7 +727,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         pl.explicit_absmax = false;
       }
     }
-    if (op.kind == OP_LINEAR && !pl.gemv)
+    if (op.kind == OP_LINEAR && !pl.gemv && op.out_f > kNarrowMaxN)
       plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, op.Kpad));
     size_t qb = op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len;
     plan->q_bytes = std::max(plan->q_bytes, qb);
@@ -939,6 +939,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         if (pl.rows > 0) {
           if (pl.gemv)
             launch_gemv(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+          else if (op.out_f <= kNarrowMaxN)
+            launch_gemm_narrow(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Kpad, ep, s);
           else
             launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
                         plan.ws.as<int32_t>(), plan.ws_bytes, s);

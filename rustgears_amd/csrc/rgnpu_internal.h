@@ -91,6 +91,11 @@ void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
 int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad);
 
 // Same contract for M <= 8 rows (weight-streaming GEMV).
+// INT8 Linear with N <= kNarrowMaxN outputs per row: one wave per row, the
+// weights from L1 (A [M,Kpad], B [>= N, Kpad]).
+constexpr int64_t kNarrowMaxN = 16;
+void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
+                        hipStream_t s);
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
                  int64_t Kpad, const Epilogue& ep, hipStream_t s);
 

@@ -157,6 +157,25 @@ def test_ragged_k_and_n(rg, ref, k, n):
     check_against_oracle(rg, ref, model.export(), rg.randn([33, k]), f"k={k} n={n}")
 
 
+@pytest.mark.parametrize("k,n,rows,act", [(4, 1, 9, "none"), (100, 2, 300, "sigmoid"), (1024, 10, 4097, "none"),
+                                          (1500, 7, 33, "gelu"), (3000, 16, 600, "relu"), (32, 3, 64, "tanh"),
+                                          (2049, 16, 9, "silu"), (256, 12, 1000, "leaky")])
+def test_narrow_outputs(rg, ref, k, n, rows, act):
+    """Linear layers with at most 16 outputs (classifier heads) on more than
+    8 rows, with their output absmax feeding a following Linear: ragged K
+    below, at and above one 1 KiB chunk, every fused activation."""
+    from rustgears_amd.inference import Activation, LayerSpec
+    a = {"relu": Activation.RELU, "sigmoid": Activation.SIGMOID, "tanh": Activation.TANH, "gelu": Activation.GELU,
+         "leaky": Activation.leaky_relu(0.1), "silu": Activation.SILU, "none": None}[act]
+    rg.manual_seed(k + 31 * n + rows)
+    layers = [LayerSpec.Linear(k, n, rg.randn([k * n]), rg.randn([n]))]
+    if a is not None:
+        layers.append(LayerSpec.Activation(a))
+    layers.append(LayerSpec.Linear(n, 40, rg.randn([n * 40]), rg.randn([40])))
+    check_against_oracle(rg, ref, layers, (rg.randn([rows, k]) * 2.0).astype(np.float32),
+                         f"narrow k={k} n={n} rows={rows} {act}")
+
+
 @pytest.mark.parametrize("act", ["relu", "sigmoid", "tanh", "gelu", "leaky", "silu", "none"])
 def test_fused_activations(rg, ref, act):
     from rustgears_amd.inference import Activation, LayerSpec
