@@ -132,7 +132,7 @@ def test_fp16_linear_activations(rg, ref, act):
     check_per_op(rg, ref, m.export(), (rg.randn([37, 200]) * 3).astype(np.float32), f"linear {act}")
 
 
-@pytest.mark.parametrize("rows", [1, 8, 255, 257, 1000])
+@pytest.mark.parametrize("rows", [1, 8, 255, 257, 1000, 4100])
 def test_fp16_rows_and_split_k(rg, ref, rows):
     """Row counts around the 256-row tile and small batches (FP16 always uses
     the MFMA GEMM; few tiles take the split-K path)."""

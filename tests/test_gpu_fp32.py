@@ -127,7 +127,7 @@ def test_fp32_deep_mlp_per_op(rg, ref):
     check_per_op(rg, ref, model.export(), x, "deep_mlp fp32")
 
 
-@pytest.mark.parametrize("rows", [1, 5, 8, 255, 700])
+@pytest.mark.parametrize("rows", [1, 5, 8, 255, 700, 4200])
 def test_fp32_rows_gemv_and_gemm(rg, ref, rows):
     from rustgears_amd import nn
     rg.manual_seed(rows + 3)
