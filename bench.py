@@ -198,8 +198,8 @@ def main():
                     help="NpuPrecision of the session (the headline metric is INT8)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (sharding is described in "
-                                   "DESIGN.md, not run)"}))
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (multi-GPU sharding is "
+                                   "designed, not built or run)"}))
         sys.exit(2)
 
     import rustgears_amd as rg

@@ -9,11 +9,12 @@
  *   InferenceSession::run                   src/inference/mod.rs:212-221
  *     -> NpuProgram::execute(&Tensor) -> (Tensor, NpuProfile)     src/inference/npu.rs:296
  * Each function below replaces one of those calls for a new provider
- * variant (ExecutionProvider::Mi355x(NpuPrecision)); INTEGRATION.md shows the
- * Rust-side binding.  All functions are thread-safe per handle: calls on one
- * program are serialized on that program's HIP stream.  No function panics or
- * throws across the ABI; failures return a nonzero status and set a
- * thread-local message readable with rgnpu_last_error().
+ * variant (ExecutionProvider::Mi355x(NpuPrecision)), bound from Rust by an
+ * extern "C" block.  All functions are thread-safe: rgnpu_program_run calls
+ * from several threads on one program run side by side on worker streams;
+ * the other calls on one program are serialized on that program's HIP stream.
+ * No function panics or throws across the ABI; failures return a nonzero
+ * status and set a thread-local message readable with rgnpu_last_error().
  */
 #ifndef RGNPU_H
 #define RGNPU_H
