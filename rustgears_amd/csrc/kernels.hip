@@ -1307,20 +1307,22 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
   }
 }
 
-// INT8 Linear with at most 16 outputs per row (the classifier heads: D's
+// Linear with at most 16 outputs per row (the classifier heads: D's
 // 1024 -> 10, C's 256 -> 10, Q's 32 -> 3).  A 128 x 128 MFMA tile would waste
 // most of its columns, so a wave takes one row at a time instead: lane l
 // holds 16 bytes of every 1 KiB K chunk of the row and of the N weight rows
-// (those are a few KiB and stay in L1), sums them with sdot4, and the wave's
-// N sums are reduce-scattered as in gemv_kernel before the fused epilogue
-// (quantize.rs:109-111; integer sums are exact in any order).
-template <int NN>
+// (those are a few KiB and stay in L1), sums them (INT8: sdot4, exact; FP16:
+// fdot2, FP32: FMA, in gemv_kernel's order), and the wave's N sums are
+// reduce-scattered as in gemv_kernel before the fused epilogue.  Kpad is in
+// bytes.
+template <int NN, int MODE>
 __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
                                                           int64_t M, int64_t N, int64_t Kpad, Epilogue ep) {
   constexpr int S = pow2_at_least(NN);
   constexpr int SPREAD = 64 / S;
   const int lane = threadIdx.x & 63;
-  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  float cs = 1.0f;
+  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int sidx = lane / SPREAD;
   const bool owner = (lane % SPREAD) == 0 && sidx < N;
   const float bias_v = ep.bias[sidx < N ? sidx : N - 1];
@@ -1341,16 +1343,38 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restri
       for (int n = 0; n < NN; n++) {
         const v4i w = *reinterpret_cast<const v4i*>(B + (int64_t)n * Kpad + kk);
         int32_t c = acc[n];
-        c = __builtin_amdgcn_sdot4(av[0], w[0], c, false);
-        c = __builtin_amdgcn_sdot4(av[1], w[1], c, false);
-        c = __builtin_amdgcn_sdot4(av[2], w[2], c, false);
-        c = __builtin_amdgcn_sdot4(av[3], w[3], c, false);
+        if constexpr (MODE == kModeF32) {
+          const v4f xf = __builtin_bit_cast(v4f, av), wf = __builtin_bit_cast(v4f, w);
+          float f = __int_as_float(c);
+#pragma unroll
+          for (int q = 0; q < 4; q++) f = __builtin_fmaf(xf[q], wf[q], f);
+          c = __float_as_int(f);
+        } else if constexpr (MODE == kModeF16) {
+          const v8h xh = __builtin_bit_cast(v8h, av), wh = __builtin_bit_cast(v8h, w);
+          float f = __int_as_float(c);
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            f = __builtin_amdgcn_fdot2(v2h{xh[2 * q], xh[2 * q + 1]}, v2h{wh[2 * q], wh[2 * q + 1]}, f, false);
+          c = __float_as_int(f);
+        } else {
+          c = __builtin_amdgcn_sdot4(av[0], w[0], c, false);
+          c = __builtin_amdgcn_sdot4(av[1], w[1], c, false);
+          c = __builtin_amdgcn_sdot4(av[2], w[2], c, false);
+          c = __builtin_amdgcn_sdot4(av[3], w[3], c, false);
+        }
         acc[n] = c;
       }
     }
-    const int32_t mine = wave_reduce_scatter<S, false>(acc, lane);
-    const float prod = (float)mine * cs;
-    const float pre = prod + bias_v;
+    const int32_t mine = wave_reduce_scatter<S, MODE != kModeI8>(acc, lane);
+    float pre;
+    if constexpr (MODE == kModeF16) {
+      pre = rgmath::round_fp16(__int_as_float(mine) + bias_v);
+    } else if constexpr (MODE == kModeF32) {
+      pre = __int_as_float(mine) + bias_v;
+    } else {
+      const float prod = (float)mine * cs;
+      pre = prod + bias_v;
+    }
     if (owner) {
       float v;
       switch (ep.act) {
@@ -1374,17 +1398,36 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restri
   }
 }
 
-void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
-                        hipStream_t s) {
-  if (N <= 0 || N > kNarrowMaxN || Kpad % 16 || Kpad <= 0) throw std::logic_error("narrow GEMM: N must be 1..16");
+template <int MODE>
+static void launch_gemm_narrow_t(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad_bytes,
+                                 const Epilogue& ep, hipStream_t s) {
+  if (N <= 0 || N > kNarrowMaxN || Kpad_bytes % 16 || Kpad_bytes <= 0)
+    throw std::logic_error("narrow GEMM: N must be 1..16 and K padded to 16 bytes");
   if (M <= 0) return;
   const int64_t blocks = std::min<int64_t>((M + 3) / 4, 8192);
   if (N <= 4)
-    RG_LAUNCH(gemm_narrow_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+    RG_LAUNCH((gemm_narrow_kernel<4, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
   else if (N <= 8)
-    RG_LAUNCH(gemm_narrow_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+    RG_LAUNCH((gemm_narrow_kernel<8, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
   else
-    RG_LAUNCH(gemm_narrow_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad, ep);
+    RG_LAUNCH((gemm_narrow_kernel<16, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
+}
+
+void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
+                        hipStream_t s) {
+  launch_gemm_narrow_t<kModeI8>(A, B, M, N, Kpad, ep, s);
+}
+
+void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
+                            const Epilogue& ep, hipStream_t s) {
+  launch_gemm_narrow_t<kModeF16>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N,
+                                 2 * Kpad_h, ep, s);
+}
+
+void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Kpad_f, const Epilogue& ep,
+                            hipStream_t s) {
+  launch_gemm_narrow_t<kModeF32>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N,
+                                 4 * Kpad_f, ep, s);
 }
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,

@@ -697,7 +697,8 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
       if (op.diag) continue;
       const int64_t es = P->precision == RGNPU_PRECISION_FP16 ? 2 : 4;
       plan->q_bytes = std::max(plan->q_bytes, (size_t)(pl.Mpad * op.Kpad * es));
-      if (!pl.gemv) plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, es * op.Kpad));
+      if (!pl.gemv && !(op.kind == OP_LINEAR && op.out_f <= kNarrowMaxN))
+        plan->ws_bytes = std::max(plan->ws_bytes, gemm_workspace_bytes(pl.Mpad, op.Npad, es * op.Kpad));
       if (op.kind == OP_CONV) plan->ylo_elems = std::max(plan->ylo_elems, (size_t)(pl.rows * op.out_f));
       continue;
     }
@@ -892,6 +893,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             pre = launch_events_used();
             if (pl.gemv)
               launch_gemv_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+            else if (op.out_f <= kNarrowMaxN)
+              launch_gemm_narrow_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, op.Kpad, ep, s);
             else
               launch_gemm_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
                               plan.ws.as<int32_t>(), plan.ws_bytes, s);
@@ -913,6 +916,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             pre = launch_events_used();
             if (pl.gemv)
               launch_gemv_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+            else if (op.out_f <= kNarrowMaxN)
+              launch_gemm_narrow_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, op.Kpad, ep, s);
             else
               launch_gemm_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
                               plan.ws.as<int32_t>(), plan.ws_bytes, s);

@@ -96,6 +96,10 @@ int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad);
 constexpr int64_t kNarrowMaxN = 16;
 void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
                         hipStream_t s);
+void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
+                            const Epilogue& ep, hipStream_t s);
+void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Kpad_f, const Epilogue& ep,
+                            hipStream_t s);
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
                  int64_t Kpad, const Epilogue& ep, hipStream_t s);
 
