@@ -430,6 +430,125 @@ __global__ __launch_bounds__(256) void nlo_to_nchw_kernel(const float* __restric
   }
 }
 
+// Direct convolution for the FP16 and FP32 providers when a window holds at
+// most kDirectConvTaps values (C * k * k: the CNN's first conv has 27).  The
+// im2col matrix would be written to HBM and fed to an MFMA tile whose
+// columns the few output channels barely fill; here one thread computes
+// every output channel of one output pixel, summing the taps serially in
+// the reference's im2col order (ch * k + ki) * k + kj, padding taps (zeros)
+// included, as fp16_gemm_fused (npu.rs:425-445) and the serial matmul of
+// conv2d_forward (kernels.rs:218-265) do.  FP16: each input is round_fp16'd
+// and each product of two binary16 values is exact in f32, so fma gives the
+// reference's multiply-then-add; the output is act(round_fp16(sum + bias)).
+// FP32: multiply, then add (no contraction); the output is sum + bias (the
+// activation is a layer of its own).  The weights of one output channel are
+// read at a wave-uniform address.
+template <int OMAX, int MODE>
+__global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restrict__ x, const void* __restrict__ wv,
+                                                          const float* __restrict__ bias, float* __restrict__ y,
+                                                          ConvShape cs, int act, float act_param) {
+  // weights as f32, tap-major [tap][OMAX] (channels past O are zero), so a
+  // tap's weights are OMAX / 4 broadcast 16-byte LDS reads
+  __shared__ __attribute__((aligned(16))) float ws[kDirectConvTaps * OMAX];
+  const int taps = (int)(cs.C * cs.k * cs.k), O = (int)cs.O, k = (int)cs.k;
+  for (int i = threadIdx.x; i < taps * OMAX; i += blockDim.x) {
+    const int kk = i / OMAX, o = i - kk * OMAX;
+    float w = 0.0f;
+    if (o < O) {
+      if constexpr (MODE == kModeF16)
+        w = (float)reinterpret_cast<const _Float16*>(wv)[(int64_t)o * cs.Kpad + kk];
+      else
+        w = reinterpret_cast<const float*>(wv)[(int64_t)o * cs.Kpad + kk];
+    }
+    ws[i] = w;
+  }
+  __syncthreads();
+  const int64_t b = blockIdx.y;
+  const int64_t L = cs.OH * cs.OW;
+  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (pix >= L) return;
+  const int oy = (int)(pix / cs.OW), ox = (int)(pix - (int64_t)oy * cs.OW);
+  const int iy0 = oy * (int)cs.stride - (int)cs.pad, ix0 = ox * (int)cs.stride - (int)cs.pad;
+  const int H = (int)cs.H, W = (int)cs.W;
+  const float* xb = x + b * cs.C * cs.H * cs.W;
+  float acc[OMAX];
+#pragma unroll
+  for (int o = 0; o < OMAX; o++) acc[o] = 0.0f;
+  int kk = 0;
+  for (int ch = 0; ch < (int)cs.C; ch++)
+    for (int ki = 0; ki < k; ki++) {
+      const int iy = iy0 + ki;
+      const bool row_ok = iy >= 0 && iy < H;
+      const float* xr = xb + ((int64_t)ch * H + iy) * W;
+      for (int kj = 0; kj < k; kj++, kk++) {
+        const int ix = ix0 + kj;
+        float v = (row_ok && ix >= 0 && ix < W) ? xr[ix] : 0.0f;
+        const float4* wr = reinterpret_cast<const float4*>(ws + kk * OMAX);
+        if constexpr (MODE == kModeF16) {
+          v = rgmath::round_fp16(v);
+#pragma unroll
+          for (int q = 0; q < OMAX / 4; q++) {
+            const float4 w4 = wr[q];
+            acc[4 * q] = __builtin_fmaf(v, w4.x, acc[4 * q]);
+            acc[4 * q + 1] = __builtin_fmaf(v, w4.y, acc[4 * q + 1]);
+            acc[4 * q + 2] = __builtin_fmaf(v, w4.z, acc[4 * q + 2]);
+            acc[4 * q + 3] = __builtin_fmaf(v, w4.w, acc[4 * q + 3]);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < OMAX / 4; q++) {
+            const float4 w4 = wr[q];
+            const float p0 = v * w4.x, p1 = v * w4.y, p2 = v * w4.z, p3 = v * w4.w;
+            acc[4 * q] = acc[4 * q] + p0;
+            acc[4 * q + 1] = acc[4 * q + 1] + p1;
+            acc[4 * q + 2] = acc[4 * q + 2] + p2;
+            acc[4 * q + 3] = acc[4 * q + 3] + p3;
+          }
+        }
+      }
+    }
+  float* yb = y + b * (int64_t)O * L + pix;
+#pragma unroll
+  for (int o = 0; o < OMAX; o++) {
+    if (o >= O) break;
+    float v;
+    if constexpr (MODE == kModeF16) {
+      const float pre = rgmath::round_fp16(acc[o] + bias[o]);
+      v = rgmath::act_apply(act, act_param, pre);
+    } else {
+      v = acc[o] + bias[o];
+    }
+    yb[(int64_t)o * L] = v;
+  }
+}
+
+template <int MODE>
+static void launch_conv_direct_t(const float* x, const void* w, const float* bias, float* y, const ConvShape& cs,
+                                 int act, float act_param, hipStream_t s) {
+  if (cs.C * cs.k * cs.k > kDirectConvTaps || cs.O > 64 || cs.O <= 0)
+    throw std::logic_error("direct conv: window or output channels too large");
+  const int64_t L = cs.OH * cs.OW;
+  if (L <= 0 || cs.n <= 0) return;
+  if (cs.n > 65535) throw std::logic_error("direct conv: too many images for one launch");
+  const dim3 grid((unsigned)((L + 255) / 256), (unsigned)cs.n);
+  if (cs.O <= 16)
+    RG_LAUNCH((conv_direct_kernel<16, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+  else if (cs.O <= 32)
+    RG_LAUNCH((conv_direct_kernel<32, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+  else
+    RG_LAUNCH((conv_direct_kernel<64, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+}
+
+void launch_conv_direct_f16(const float* x, const uint16_t* w, const float* bias, float* y, const ConvShape& cs,
+                            int act, float act_param, hipStream_t s) {
+  launch_conv_direct_t<kModeF16>(x, w, bias, y, cs, act, act_param, s);
+}
+
+void launch_conv_direct_f32(const float* x, const float* w, const float* bias, float* y, const ConvShape& cs,
+                            hipStream_t s) {
+  launch_conv_direct_t<kModeF32>(x, w, bias, y, cs, rgmath::ACT_NONE, 0.0f, s);
+}
+
 void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s) {
   const int64_t total = n * O * L;
   if (total <= 0) return;

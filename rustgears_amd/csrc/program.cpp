@@ -957,7 +957,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         const ConvShape& c = pl.cs;
         if (f32) {  // mod.rs:274-290: conv2d_forward (im2col + matmul), then the bias
           pre = launch_events_used();
-          if (pl.rows > 0) {
+          if (pl.rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64) {
+            launch_conv_direct_f32(in, op.d_w.as<float>(), op.d_bias.as<float>(), out, c, s);
+          } else if (pl.rows > 0) {
             float* a = plan.q.as<float>();
             launch_im2col_f32(in, c, pl.Mpad, op.Kpad, a, s);
             Epilogue ep;
@@ -972,7 +974,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         }
         if (f16) {  // npu.rs:341-376: im2col, GEMM, transpose per image
           pre = launch_events_used();
-          if (pl.rows > 0) {
+          if (pl.rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64) {
+            launch_conv_direct_f16(in, op.d_w.as<uint16_t>(), op.d_bias.as<float>(), out, c, op.act, op.act_param, s);
+          } else if (pl.rows > 0) {
             uint16_t* h = plan.q.as<uint16_t>();
             launch_im2col_half(in, c, pl.Mpad, op.Kpad, h, s);
             Epilogue ep;

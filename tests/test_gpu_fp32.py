@@ -162,3 +162,22 @@ def test_fp32_report(rg, ref):
     # compilation_report of a Standard program (mod.rs:198-204): 3 folded layers from 4 raw ones
     assert sess.compilation_report() == "InferenceSession [provider = GPU:0 (FP32), device = gpu:0, ops = 3 (from 4 raw layers)]"
     sess.close()
+
+
+@pytest.mark.parametrize("spec", [(3, 32, 3, 1, 1), (2, 5, 3, 2, 0), (1, 64, 5, 1, 2), (7, 4, 2, 1, 0), (3, 17, 3, 3, 1)])
+def test_fp32_direct_conv_exact(rg, ref, spec):
+    """A convolution whose window holds at most 32 values runs as a direct
+    conv that sums the taps in the reference's serial im2col order, so it is
+    bit-exact with the oracle (not only within the reordering bound)."""
+    from rustgears_amd import nn
+    C, O, k, s, p = spec
+    rg.manual_seed(C * 100 + O * 10 + k)
+    m = nn.Sequential().add(nn.Conv2d(C, O, k).stride(s).padding(p)).add(nn.Relu())
+    layers = m.export()
+    x = (rg.randn([4, C, 11, 13]) * 2.0).astype(np.float32)
+    print(f"[direct conv fp32] {spec}", flush=True)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.Gpu(0))
+    y = sess.run(x)
+    want = ref.RefProgram(layers, precision=ref.FP32).run(x)
+    assert_bitexact_f32(y, want, f"direct conv {spec}")
+    sess.close()
