@@ -336,6 +336,42 @@ def test_consecutive_runs_on_one_session(rg, ref, kind):
     sess.close()
 
 
+def test_reference_integration_model(rg, ref):
+    """The reference's own NPU integration test (integration.rs:127-164) on the
+    MI355X provider: 9 raw layers fuse to 5 ops with the reference's labels,
+    the weights compress more than 3x, the INT8 output stays within 0.15 of
+    the fp32 model (BN statistics warmed by one training forward), and it is
+    bit-exact with the oracle."""
+    from test_oracle import _bn_eval, _bn_train_update, _np_conv
+    from rustgears_amd import nn
+    rg.manual_seed(2026)
+    conv, bn2 = nn.Conv2d(1, 4, 3).padding(1), nn.BatchNorm2d(4)
+    l1, bn1, l2 = nn.Linear(64, 16), nn.BatchNorm1d(16), nn.Linear(16, 4)
+    model = (nn.Sequential().add(conv).add(bn2).add(nn.Relu()).add(nn.MaxPool2d(2)).add(nn.Flatten())
+             .add(l1).add(bn1).add(nn.Relu()).add(l2))
+    x = rg.randn([8, 1, 8, 8])
+    xd = x.astype(np.float64)
+    h = _np_conv(xd, conv.weight.astype(np.float64), conv.bias.astype(np.float64), 1)
+    h = np.maximum(_bn_train_update(bn2, h), 0)
+    h = h.reshape(8, 4, 4, 2, 4, 2).max(axis=(3, 5)).reshape(8, 64)
+    _bn_train_update(bn1, h @ l1.weight + l1.bias)
+    h = _np_conv(xd, conv.weight.astype(np.float64), conv.bias.astype(np.float64), 1)
+    h = np.maximum(_bn_eval(bn2, h), 0)
+    h = h.reshape(8, 4, 4, 2, 4, 2).max(axis=(3, 5)).reshape(8, 64)
+    fp32 = np.maximum(_bn_eval(bn1, h @ l1.weight + l1.bias), 0) @ l2.weight + l2.bias
+    layers = model.export()
+    y = check_against_oracle(rg, ref, layers, x, "integration.rs model")
+    sess = make_session(rg, layers)
+    sess.run(x)
+    prof = sess.last_npu_profile()
+    assert prof.original_layers == 9 and prof.fused_ops == 5
+    assert prof.compression_ratio() > 3.0
+    assert [r.op for r in prof.records] == ["NPU::FusedConv2dAct(1->4, k=3, ReLU)", "NPU::MaxPool2d(k=2)",
+                                            "NPU::Flatten", "NPU::FusedGemmAct(64->16, ReLU)", "NPU::Gemm(16->4)"]
+    assert np.abs(y - fp32).max() <= 0.15
+    sess.close()
+
+
 def test_compilation_report(rg, ref):
     from rustgears_amd import nn
     rg.manual_seed(0)
