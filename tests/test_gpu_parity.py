@@ -336,6 +336,67 @@ def test_consecutive_runs_on_one_session(rg, ref, kind):
     sess.close()
 
 
+def _random_model(seed):
+    """A seeded random layer stack: an optional conv section (1-2 convs with
+    random channels, window 1/2/3/5, stride 1/2, padding 0-2, each optionally
+    followed by a folding ChannelAffine, an activation and a max pool),
+    Flatten, then 1-3 Linears with the same optional extras, an optional lone
+    ChannelAffine at the start of the dense section and an optional Softmax."""
+    from rustgears_amd.inference import Activation, LayerSpec
+    g = np.random.default_rng(seed)
+    acts = [Activation.RELU, Activation.SIGMOID, Activation.TANH, Activation.GELU, Activation.leaky_relu(0.2),
+            Activation.SILU, Activation.NONE]
+    f32 = lambda a: np.asarray(a, np.float32)
+    layers = []
+    if g.random() < 0.5:
+        n, C, H, W = int(g.choice([1, 2, 5, 16])), int(g.integers(1, 20)), int(g.integers(4, 20)), int(g.integers(4, 20))
+        shape = [n, C, H, W]
+        for _ in range(int(g.integers(1, 3))):
+            O, k, st, pd = int(g.integers(1, 48)), int(g.choice([1, 2, 3, 5])), int(g.choice([1, 2])), int(g.integers(0, 3))
+            if H + 2 * pd < k or W + 2 * pd < k:
+                k = 1
+            layers.append(LayerSpec.Conv2d(C, O, k, st, pd, f32(g.standard_normal(O * C * k * k) / np.sqrt(C * k * k)),
+                                           f32(g.standard_normal(O) * 0.1)))
+            H, W, C = (H + 2 * pd - k) // st + 1, (W + 2 * pd - k) // st + 1, O
+            if g.random() < 0.4:
+                layers.append(LayerSpec.ChannelAffine(f32(g.uniform(0.5, 1.5, C)), f32(g.standard_normal(C) * 0.1)))
+            if g.random() < 0.7:
+                layers.append(LayerSpec.Activation(acts[int(g.integers(0, len(acts)))]))
+            if g.random() < 0.5 and min(H, W) >= 2:
+                pk = 3 if min(H, W) >= 3 and g.random() < 0.3 else 2
+                ps = int(g.choice([1, 2]))
+                layers.append(LayerSpec.MaxPool2d(pk, ps))
+                H, W = (H - pk) // ps + 1, (W - pk) // ps + 1
+        layers.append(LayerSpec.Flatten())
+        F = C * H * W
+    else:
+        rows, F = int(g.choice([1, 3, 8, 9, 64, 300, 513])), int(g.integers(1, 700))
+        shape = [rows, F]
+        if g.random() < 0.2:
+            layers.append(LayerSpec.ChannelAffine(f32(g.uniform(0.5, 1.5, F)), f32(g.standard_normal(F) * 0.1)))
+    for _ in range(int(g.integers(1, 4))):
+        out = int(g.choice([1, 3, 10, 16, 17, 64, 130, 300]))
+        layers.append(LayerSpec.Linear(F, out, f32(g.standard_normal(F * out) / np.sqrt(F)), f32(g.standard_normal(out) * 0.1)))
+        F = out
+        if g.random() < 0.3:
+            layers.append(LayerSpec.ChannelAffine(f32(g.uniform(0.5, 1.5, F)), f32(g.standard_normal(F) * 0.1)))
+        if g.random() < 0.7:
+            layers.append(LayerSpec.Activation(acts[int(g.integers(0, len(acts)))]))
+    if g.random() < 0.3:
+        layers.append(LayerSpec.Softmax())
+    x = f32(g.standard_normal(shape) * float(g.choice([0.5, 1.0, 3.0])))
+    return layers, x
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_models(rg, ref, seed):
+    """Seeded random layer stacks through the whole plan (buffer ping-pong,
+    slot layout, fusion and folding rules, every kernel choice): every op
+    bit-exact with the oracle."""
+    layers, x = _random_model(1000 + seed)
+    check_against_oracle(rg, ref, layers, x, f"random model {seed}: {[type(l).__name__ for l in layers]}")
+
+
 def test_reference_integration_model(rg, ref):
     """The reference's own NPU integration test (integration.rs:127-164) on the
     MI355X provider: 9 raw layers fuse to 5 ops with the reference's labels,
