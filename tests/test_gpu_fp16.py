@@ -227,3 +227,13 @@ def test_fp16_direct_conv_exact(rg, ref, spec):
     want = ref.RefProgram(layers, precision=ref.FP16).run(x)
     assert_bitexact_f32(y, want, f"direct conv {spec}")
     sess.close()
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_fp16_random_models(rg, ref, seed):
+    """The INT8 suite's seeded random layer stacks on this provider: every
+    Linear/Conv op within the summation-order bound, every other op bit for
+    bit."""
+    from test_gpu_parity import _random_model
+    layers, x = _random_model(1000 + seed)
+    check_per_op(rg, ref, layers, x, f"random model {seed}")
