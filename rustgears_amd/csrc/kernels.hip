@@ -340,6 +340,7 @@ __device__ __forceinline__ uint32_t half2_of(float a, float b) {
   return (uint32_t)rgmath::fp16_bits(rgmath::round_fp16(a)) | ((uint32_t)rgmath::fp16_bits(rgmath::round_fp16(b)) << 16);
 }
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void half_rows_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                         int64_t Mpad, int64_t Kpad_h, uint16_t* __restrict__ h) {
   const uint32_t chunks = (uint32_t)(Kpad_h / 8);
@@ -351,8 +352,13 @@ __global__ __launch_bounds__(256) void half_rows_kernel(const float* __restrict_
     if (r < M) {
       const float* xr = x + r * K;
       float v[8];
+      if (VEC && c0 + 8 <= (uint32_t)K) {
+        const float4 p = reinterpret_cast<const float4*>(xr + c0)[0], q = reinterpret_cast<const float4*>(xr + c0)[1];
+        v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = q.x; v[5] = q.y; v[6] = q.z; v[7] = q.w;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[e] = c0 + (uint32_t)e < (uint32_t)K ? xr[c0 + e] : 0.0f;
+        for (int e = 0; e < 8; e++) v[e] = c0 + (uint32_t)e < (uint32_t)K ? xr[c0 + e] : 0.0f;
+      }
 #pragma unroll
       for (int g = 0; g < 4; g++) out[g] = (int)half2_of(v[2 * g], v[2 * g + 1]);
     }
@@ -360,12 +366,18 @@ __global__ __launch_bounds__(256) void half_rows_kernel(const float* __restrict_
   }
 }
 
+// Rows whose K is a multiple of 4 on a 16-byte aligned base are read with
+// 16-byte loads.
 void launch_half_rows(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad_h, uint16_t* h, hipStream_t s) {
   const int64_t chunks = Mpad * (Kpad_h / 8);
   if (chunks <= 0) return;
   int64_t blocks = (chunks + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  RG_LAUNCH(half_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_h, h);
+  const bool vec = (K % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (vec)
+    RG_LAUNCH(half_rows_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_h, h);
+  else
+    RG_LAUNCH(half_rows_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_h, h);
 }
 
 // im2col in binary16 for the FP16 conv (npu.rs:341-355): row img*L + oy*OW + ox,
@@ -562,6 +574,7 @@ void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float
 // (one thread per 4 floats), and im2col in f32 with the reference's column
 // order (kernels.rs:28-96).
 // ---------------------------------------------------------------------------
+template <bool VEC>
 __global__ __launch_bounds__(256) void pad_rows_f32_kernel(const float* __restrict__ x, int64_t M, int64_t K,
                                                            int64_t Mpad, int64_t Kpad_f, float* __restrict__ a) {
   const uint32_t chunks = (uint32_t)(Kpad_f / 4);
@@ -572,10 +585,14 @@ __global__ __launch_bounds__(256) void pad_rows_f32_kernel(const float* __restri
     float4 out = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (r < M) {
       const float* xr = x + r * K;
-      out.x = c0 < (uint32_t)K ? xr[c0] : 0.0f;
-      out.y = c0 + 1 < (uint32_t)K ? xr[c0 + 1] : 0.0f;
-      out.z = c0 + 2 < (uint32_t)K ? xr[c0 + 2] : 0.0f;
-      out.w = c0 + 3 < (uint32_t)K ? xr[c0 + 3] : 0.0f;
+      if (VEC && c0 + 4 <= (uint32_t)K) {
+        out = *reinterpret_cast<const float4*>(xr + c0);
+      } else {
+        out.x = c0 < (uint32_t)K ? xr[c0] : 0.0f;
+        out.y = c0 + 1 < (uint32_t)K ? xr[c0 + 1] : 0.0f;
+        out.z = c0 + 2 < (uint32_t)K ? xr[c0 + 2] : 0.0f;
+        out.w = c0 + 3 < (uint32_t)K ? xr[c0 + 3] : 0.0f;
+      }
     }
     reinterpret_cast<float4*>(a)[w] = out;
   }
@@ -586,7 +603,10 @@ void launch_pad_rows_f32(const float* x, int64_t M, int64_t K, int64_t Mpad, int
   if (chunks <= 0) return;
   int64_t blocks = (chunks + 255) / 256;
   if (blocks > 8192) blocks = 8192;
-  RG_LAUNCH(pad_rows_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_f, a);
+  if ((K % 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0)
+    RG_LAUNCH(pad_rows_f32_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_f, a);
+  else
+    RG_LAUNCH(pad_rows_f32_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, s, x, M, K, Mpad, Kpad_f, a);
 }
 
 __global__ __launch_bounds__(256) void im2col_f32_kernel(const float* __restrict__ x, ConvShape cs, int64_t Mpad,

@@ -885,8 +885,14 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         if (f32) {  // mod.rs:263-273: matmul, then the bias
           pre = launch_events_used();
           if (pl.rows > 0) {
-            float* a = plan.q.as<float>();
-            launch_pad_rows_f32(in, pl.rows, op.K, pl.Mpad, op.Kpad, a, s);
+            // the GEMM reads [Mpad, Kpad] rows: an input of exactly that shape
+            // on a 16-byte boundary is read in place
+            const float* a = in;
+            if (pl.rows != pl.Mpad || op.K != op.Kpad || (reinterpret_cast<uintptr_t>(in) & 15) != 0) {
+              float* pa = plan.q.as<float>();
+              launch_pad_rows_f32(in, pl.rows, op.K, pl.Mpad, op.Kpad, pa, s);
+              a = pa;
+            }
             Epilogue ep;
             ep.bias = op.d_bias.as<float>();
             ep.y = out;
