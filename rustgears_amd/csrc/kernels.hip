@@ -58,12 +58,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
-__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
 __device__ __forceinline__ float slot_scale(const uint32_t* slot) {
   return rgmath::scale_from_absmax(rgmath::bitsf(*slot));
 }
