@@ -281,7 +281,6 @@ RG_HD float gelu_fast(float x) {
   const float ln2_hi = bitsf(0x3f317180u), ln2_lo = bitsf(0x3717f7d1u), invln2 = bitsf(0x3fb8aa3bu);
   const float Q1 = bitsf(0xbd088889u), Q2 = bitsf(0x3ad00d01u), Q3 = bitsf(0xb8a670cdu),
               Q4 = bitsf(0x36867e54u), Q5 = bitsf(0xb457edbbu);
-  const uint32_t hx = fbits(arg) & 0x7fffffffu;
   float kf = invln2 * arg;
   kf = kf + (ge1 ? 0.5f : -0.5f);
   const int32_t k = (int32_t)kf;
