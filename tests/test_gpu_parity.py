@@ -263,6 +263,43 @@ def test_shape_changes_and_errors(rg, ref):
         conv.run(np.ones((1, 3, 2, 2), np.float32))
 
 
+@pytest.mark.parametrize("prec", ["int8", "fp16", "fp32"])
+def test_empty_batch(rg, ref, prec):
+    """Zero rows or images: the reference's quantize of an empty tensor takes
+    scale 1 (quantize.rs:19-21) and every op yields an empty output of the
+    right shape.  Nothing is launched for the empty ops, capture taps are
+    empty, and the session (and its absmax slots) stays exact for the
+    non-empty runs that follow."""
+    from rustgears_amd import nn
+    from rustgears_amd.inference import Activation, LayerSpec
+    provider = {"int8": rg.ExecutionProvider.mi355x_int8(), "fp16": rg.ExecutionProvider.mi355x_fp16(),
+                "fp32": rg.ExecutionProvider.Gpu(0)}[prec]
+    rg.manual_seed(41)
+    mlp = nn.Sequential().add(nn.Linear(300, 260)).add(nn.Gelu()).add(nn.Linear(260, 7)).export()
+    cnn = (nn.Sequential().add(nn.Conv2d(3, 8, 3).padding(1)).add(nn.Relu()).add(nn.MaxPool2d(2))
+           .add(nn.Conv2d(8, 40, 3)).add(nn.MaxPool2d(2)).add(nn.Flatten()).add(nn.Linear(40, 5)).export())
+    tail = mlp + [LayerSpec.Activation(Activation.TANH), LayerSpec.Softmax()]
+    for name, layers, shape in (("mlp", mlp, (300,)), ("cnn", cnn, (3, 8, 8)), ("softmax tail", tail, (300,))):
+        print(f"[parity] empty batch {prec} {name}", flush=True)
+        sess = rg.InferenceSession.from_layers(layers, provider)
+        p = ref.RefProgram(layers, precision={"int8": ref.INT8, "fp16": ref.FP16, "fp32": ref.FP32}[prec])
+        x0 = np.zeros((0,) + shape, np.float32)
+        x = rg.randn([5] + list(shape))
+        want = sess.run(x)
+        for capture in (False, True):
+            sess.set_capture(capture)
+            y0 = sess.run(x0)
+            assert y0.shape == p.run(x0).shape and y0.size == 0, f"{name}: {y0.shape}"
+            assert_bitexact_f32(sess.run(x), want, f"{name}: run after an empty one (capture {capture})")
+        sess.set_capture(False)
+        dx, dy = rg.DeviceBuffer(4), rg.DeviceBuffer(4)
+        assert sess.run_device(dx, x0.shape, dy) == y0.shape
+        sess.synchronize()
+        if prec == "int8":
+            assert_bitexact_f32(want, p.run(x), f"{name} vs oracle")
+        sess.close()
+
+
 def test_device_resident_run_matches_host_run(rg, ref):
     from rustgears_amd import configs
     model, x = configs.deep_mlp(rows=512)
