@@ -265,17 +265,19 @@ RG_HD float tanhf_fast(float x) {
 //    which 1 + t absorbs;
 //  * expm1's k selection: k = 0 below 0.5 ln2 comes out of the rounded
 //    reduction except at its boundary, where the result is unchanged;
-//  * expm1's reconstruction for k <= -2 and for 3 <= k <= 27 is one formula
-//    y = T - (e - x), y * 2^k, minus 1 when k < 0 (T = 1 or 1 - 2^-k); the
+//  * expm1's reconstruction for k <= -2, k == 0 and 3 <= k <= 27 is one
+//    formula y = T - (e - x), y * 2^k, minus 1 when k < 0 (T = 1, 0 or
+//    1 - 2^-k); for k == 0 it is fdlibm's x - (x*e - hxs) exactly, and the
 //    23 <= k form x - (e + 2^-k) + 1 gives the same GELU.
 // The exhaustive device check (every f32 input) confirms gelu_fast == gelu.
 RG_HD float gelu_fast(float x) {
   float x3 = 0.044715f * x; x3 = x3 * x; x3 = x3 * x;
   const float inner = x + x3;
   const float u = 0.7978846f * inner;
-  const uint32_t ju = fbits(u), iu = ju & 0x7fffffffu;
-  const bool ge1 = iu >= 0x3f800000u;
-  const float two_au = 2.0f * bitsf(iu);
+  const uint32_t ju = fbits(u);
+  const float au = __builtin_fabsf(u);
+  const bool ge1 = !(au < 1.0f);  // |u| >= 1 or NaN, as the integer test of |u|'s bits
+  const float two_au = 2.0f * au;
   // tanhf: t = expm1(2|u|) for |u| >= 1, expm1(-2|u|) below
   const float arg = ge1 ? __builtin_fminf(two_au, 18.5f) : -two_au;
   const float ln2_hi = bitsf(0x3f317180u), ln2_lo = bitsf(0x3717f7d1u), invln2 = bitsf(0x3fb8aa3bu);
@@ -304,10 +306,8 @@ RG_HD float gelu_fast(float x) {
   const float den = 6.0f - xt;
   const float num = r1 - tt;
   const float e = hxs * div_fast(num, den);
-  // k == 0
-  const float xe = xr * e;
-  const float r0 = xr - (xe - hxs);
-  // k != 0: e2 = x*(e-c) - c - hxs
+  // e2 = x*(e-c) - c - hxs, em = e2 - x.  For k == 0, c is exactly 0, so
+  // -em is fdlibm's x - (x*e - hxs) bit for bit.
   const float ec = e - c;
   float e2 = xr * ec;
   e2 = e2 - c;
@@ -316,12 +316,14 @@ RG_HD float gelu_fast(float x) {
   // k == -1
   const float d1 = xr - e2;
   const float rm1 = 0.5f * d1 - 0.5f;
-  // k <= -2 and 3 <= k <= 27
-  const float T = k < 0 ? 1.0f : bitsf(0x3f800000u - (0x1000000u >> (k & 31)));
-  const float y = T - em;
+  // k <= -2, k == 0 and 3 <= k <= 27: y = T - em scaled by 2^k, minus 1
+  // when k < 0, with T = 1 - 2^-k (0 for k == 0, exact up to k = 24, 1 from
+  // k = 25 on) and T = 1 for k < 0 (the shift by k & 31 >= 29 gives 0)
+  const float T = bitsf(0x3f800000u - (0x1000000u >> (k & 31)));
+  const float y = (k == 0 ? 0.0f : T) - em;
   const float ys = bitsf(fbits(y) + ((uint32_t)k << 23));
   const float rk = k < 0 ? ys - 1.0f : ys;
-  const float t = k == 0 ? r0 : (k == -1 ? rm1 : rk);
+  const float t = k == -1 ? rm1 : rk;
   // tanhf: z = 1 - 2/(t+2) for |u| >= 1, -t/(t+2) below; sign of u
   const float d = t + 2.0f;
   const float q = div_fast(ge1 ? 2.0f : -t, d);

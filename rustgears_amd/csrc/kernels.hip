@@ -855,22 +855,32 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
+// Raw buffer resource over base (gfx9 word 3: 32-bit data format); the
+// record count is left at its maximum, so no store is clipped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, -1, 0x00020000);
+}
+
+// One staged 16-row slab: rows (wave-uniform) outputs per lane, row r at
+// yrow + r N, byte offset col_bytes.  The stores are buffer stores with the
+// row's byte offset r N 4 in a scalar register and the lane's column in a
+// 32-bit vector offset (both fit: N <= 2^26), so the loop counter and all
+// row addressing stay scalar.  Returns the running max of |y| (NaN ignored,
+// like f32::max), as f32.
 template <int ACT, bool CAP, int MODE>
-__device__ __forceinline__ uint32_t big_epilogue_slab(const int32_t* slab, int rows, float* yp, int32_t* ap, int64_t N,
-                                                      float cs, float b, float p, int lane) {
-  uint32_t amax = 0;
-#pragma unroll 1
+__device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows, float* yrow, int32_t* arow,
+                                                   int64_t N, uint32_t col_bytes, float cs, float b, float p,
+                                                   int lane, float amax) {
+  const __amdgpu_buffer_rsrc_t ry = raw_rsrc(yrow);
+  const __amdgpu_buffer_rsrc_t ra = raw_rsrc(arow);
+  const uint32_t row_bytes = (uint32_t)N * 4u;
+#pragma unroll 4
   for (int r = 0; r < rows; r++) {
     const int32_t a = slab[r * big::SLAB_LD + lane];
     const float v = epi_word<ACT, MODE>(a, cs, b, p);
-    *yp = v;
-    yp += N;
-    if (CAP) {
-      *ap = a;
-      ap += N;
-    }
-    const uint32_t k = rgmath::absmax_key(v);
-    amax = k > amax ? k : amax;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, (int)col_bytes, (int)(r * row_bytes), 0);
+    if (CAP) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)a, ra, (int)col_bytes, (int)(r * row_bytes), 0);
+    amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
   }
   return amax;
 }
@@ -884,10 +894,10 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
                                                  int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                  int wave, int wm, int wn, int lane) {
   int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
-  uint32_t amax = 0;
+  float amax = 0.0f;
   const int64_t col = n0 + wn * 64 + lane;
   // Every lane stages its accumulators (the slab is shared by the wave);
-  // lanes past the last column then store nothing.
+  // lanes past the last column then skip the slab loop.
   const bool col_ok = col < N;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
@@ -896,13 +906,12 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
 #pragma unroll
       for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
     const int64_t row0 = m0 + wm * (16 * FM) + i * 16;
-    const int rows = col_ok ? (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16) : 0;
-    float* yp = ep.y + row0 * N + col;
-    int32_t* ap = CAP ? ep.acc_out + row0 * N + col : nullptr;
-    const uint32_t a = big_epilogue_slab<ACT, CAP, MODE>(slab, rows, yp, ap, N, cs, b, ep.act_param, lane);
-    amax = a > amax ? a : amax;
+    const int rows = (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16);
+    if (col_ok)
+      amax = big_epilogue_slab<ACT, CAP, MODE>(slab, rows, ep.y + row0 * N, CAP ? ep.acc_out + row0 * N : nullptr, N,
+                                               (uint32_t)col * 4u, cs, b, ep.act_param, lane, amax);
   }
-  return amax;
+  return rgmath::fbits(amax);
 }
 
 template <int ACT, int FM, int MODE>
@@ -934,7 +943,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
   constexpr int A_ST = BM * BK, ST = (BM + BN) * BK;
   static_assert(NW * SLAB <= STAGES * ST, "epilogue slabs reuse the ring");
   __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index read through a scalar register: the compiler then keeps the
+  // wave's tile coordinates and row bases scalar
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   int tile_m, tile_n;

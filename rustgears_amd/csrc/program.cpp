@@ -201,6 +201,8 @@ static void check_layer(const rgnpu_layer& l, int64_t idx) {
   switch (l.kind) {
     case RGNPU_LAYER_LINEAR:
       if (l.in_features <= 0 || l.out_features <= 0) bad("Linear needs positive in/out features");
+      // the GEMM epilogue addresses 16 output rows with 32-bit byte offsets
+      if (l.out_features > (1 << 26)) bad("Linear out_features above 2^26 are not supported");
       if (l.weight_len != (int64_t)l.in_features * l.out_features || !l.weight) bad("Linear weight must be [in, out]");
       if (l.bias_len != l.out_features || !l.bias) bad("Linear bias must have out_features elements");
       break;
