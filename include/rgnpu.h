@@ -105,7 +105,9 @@ typedef struct rgnpu_profile {
  * reference's serial f32 loop (npu.rs:433-445), so its results agree within
  * that reordering (see the test suite's bound), and an activation or weight
  * whose round_fp16 value is +-65536 (inputs in [65520, 65536)) saturates to
- * +-65504, the largest binary16 value. */
+ * +-65504, the largest binary16 value.  A Linear layer may have at most
+ * 2^26 output features (RGNPU_ERR_INVALID above that; the reference has no
+ * such limit). */
 int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t precision,
                          int32_t device, rgnpu_program** out);
 
