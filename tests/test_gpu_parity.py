@@ -261,6 +261,12 @@ def test_shape_changes_and_errors(rg, ref):
         conv.run(np.ones((1, 2, 5, 5), np.float32))
     with pytest.raises(rg.RgnpuError):
         conv.run(np.ones((1, 3, 2, 2), np.float32))
+    # the documented output-feature limit of a Linear layer (2^26)
+    from rustgears_amd.inference import LayerSpec
+    n_big = (1 << 26) + 1
+    with pytest.raises(rg.RgnpuError) as e:
+        make_session(rg, [LayerSpec.Linear(1, n_big, np.zeros(n_big, np.float32), np.zeros(n_big, np.float32))])
+    assert "2^26" in str(e.value)
 
 
 @pytest.mark.parametrize("prec", ["int8", "fp16", "fp32"])
