@@ -137,6 +137,25 @@ def dominant_roofline(name, records, layers, x, workload, prec="int8"):
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 
+def host_description() -> dict:
+    """CPU model and glibc version of the host the baseline ran on (the
+    oracle's GELU, Sigmoid and Tanh follow the host libm)."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = ""
+    return {"cpu": model, "logical_cpus": os.cpu_count(), "libc": libc}
+
+
 def cpu_baseline(name, layers, x, target_s: float, prec="int8"):
     """The oracle (C restatement of the reference's rayon INT8 path, or of
     its FP16 path) on a bounded sample of the same workload, all host
@@ -296,6 +315,7 @@ def main():
         "runs": n_conc, "note": "host-pointer run() from several threads on one session, wall clock"}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, args.precision)
+        line["cpu_baseline"]["host"] = host_description()
     print(json.dumps(line), flush=True)
 
 
