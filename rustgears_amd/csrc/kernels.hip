@@ -159,14 +159,6 @@ void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s) {
 // The unmasked form streams 16-byte loads; the masked form (conv inputs whose
 // rows/columns are not all read by a window) tests each element's position.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t max4_key(float4 v, uint32_t m) {
-  uint32_t a = rgmath::absmax_key(v.x), b = rgmath::absmax_key(v.y);
-  uint32_t c = rgmath::absmax_key(v.z), d = rgmath::absmax_key(v.w);
-  a = a > b ? a : b;
-  c = c > d ? c : d;
-  a = a > c ? a : c;
-  return a > m ? a : m;
-}
 
 // One atomic per block: into `slot` itself, or (spread) into the block's
 // partial of a spread slot.
@@ -201,23 +193,34 @@ __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x
   uint32_t m = 0;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // 16-byte path when the image start is aligned, then the tail
+  // Aligned images: each thread reads contiguous 64-byte chunks (a wave
+  // covers 4 KiB), two chunks per iteration; then the tail.  The running
+  // max is kept as f32 (NaN ignored, like f32::max) and its bits are the key.
   const bool al = (reinterpret_cast<uintptr_t>(xi) & 15) == 0;
-  const int64_t n4 = al ? per_img / 4 : 0;
+  const int64_t n16 = al ? per_img / 16 : 0;
   const float4* x4 = reinterpret_cast<const float4*>(xi);
-  int64_t i = tid;
-  for (; i + 3 * stride < n4; i += 4 * stride) {
-    const float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
-    m = max4_key(a, m);
-    m = max4_key(b, m);
-    m = max4_key(c, m);
-    m = max4_key(d, m);
+  float fm = 0.0f;
+  auto take4 = [&](float4 v) {
+    fm = __builtin_fmaxf(fm, __builtin_fabsf(v.x));
+    fm = __builtin_fmaxf(fm, __builtin_fabsf(v.y));
+    fm = __builtin_fmaxf(fm, __builtin_fabsf(v.z));
+    fm = __builtin_fmaxf(fm, __builtin_fabsf(v.w));
+  };
+  int64_t c = tid;
+  for (; c + stride < n16; c += 2 * stride) {
+    const float4* p = x4 + c * 4;
+    const float4* q = x4 + (c + stride) * 4;
+    const float4 a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+    const float4 b0 = q[0], b1 = q[1], b2 = q[2], b3 = q[3];
+    take4(a0); take4(a1); take4(a2); take4(a3);
+    take4(b0); take4(b1); take4(b2); take4(b3);
   }
-  for (; i < n4; i += stride) m = max4_key(x4[i], m);
-  for (int64_t e = n4 * 4 + tid; e < per_img; e += stride) {
-    const uint32_t k = rgmath::absmax_key(xi[e]);
-    m = k > m ? k : m;
+  if (c < n16) {
+    const float4* p = x4 + c * 4;
+    take4(p[0]); take4(p[1]); take4(p[2]); take4(p[3]);
   }
+  for (int64_t e = n16 * 16 + tid; e < per_img; e += stride) fm = __builtin_fmaxf(fm, __builtin_fabsf(xi[e]));
+  m = rgmath::fbits(fm);
   block_max_atomic(m, spread ? slots : &slots[img], spread != 0);
 }
 
@@ -247,8 +250,8 @@ void launch_absmax(const float* x, int64_t per_img, int64_t n_img, uint32_t* slo
                    SlotClear clear) {
   if (per_img <= 0 || n_img <= 0) return;
   if (spread && (n_img != 1 || rowmask)) throw std::logic_error("spread absmax takes one unmasked tensor");
-  int64_t bx = (per_img + 256 * 16 - 1) / (256 * 16);
-  const int64_t cap = n_img >= 64 ? 8 : 2048;
+  int64_t bx = (per_img + 256 * 32 - 1) / (256 * 32);
+  const int64_t cap = n_img >= 64 ? 8 : 4096;
   if (bx > cap) bx = cap;
   if (bx < 1) bx = 1;
   if (rowmask)
