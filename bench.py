@@ -78,11 +78,15 @@ def build_workload(name: str, batch: int, stack_act: str = "gelu", gemv_act: str
     raise SystemExit(f"unknown workload {name}")
 
 
-def measured_traffic(workload: str, kernel: str):
+def measured_traffic(workload: str, kernel: str, prec: str = "int8"):
     """HBM bytes per launch of `kernel` in `workload` from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.txt:
     lines `workload<TAB>kernel label<TAB>bytes`, already scaled by the copy
-    calibration); None when that pair was not profiled."""
+    calibration; the workload carries an `@fp16` / `@fp32` suffix for the
+    other precisions, whose op labels can equal the INT8 ones); None when
+    that pair was not profiled."""
+    if prec != "int8":
+        workload = f"{workload}@{prec}"
     path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
     if not os.path.exists(path):
         return None
@@ -105,7 +109,6 @@ PRECISIONS = {
 def dominant_roofline(name, records, layers, x, workload, prec="int8"):
     """Roofline of the dominant kernel (largest total kernel time per step)."""
     _, peak, _, eb, _ = PRECISIONS[prec]
-    fp16 = prec != "int8"  # HBM traffic was measured for the INT8 kernels only
     best = max(range(len(records)), key=lambda i: records[i].kernel_ns)
     r = records[best]
     if r.kernel_ns <= 0:
@@ -121,19 +124,19 @@ def dominant_roofline(name, records, layers, x, workload, prec="int8"):
         byts = eb * li.in_features * li.out_features + 4 * li.out_features + eb * b * li.in_features + 4 * b * li.out_features
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None if fp16 else measured_traffic(workload, r.op),
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec),
                 "kernel": r.op, "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     if r.macs == 0:
         # elementwise op (copy calibration): f32 in + f32 out
         byts = 8 * int(np.prod(x.shape))
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op), "kernel": r.op,
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec), "kernel": r.op,
                 "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     ops = 2 * r.macs
     ach = ops / secs / 1e12
     return {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(ach / peak, 4), "traffic": None if fp16 else measured_traffic(workload, r.op), "kernel": r.op,
+            "frac": round(ach / peak, 4), "traffic": measured_traffic(workload, r.op, prec), "kernel": r.op,
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 
