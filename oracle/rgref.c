@@ -73,10 +73,16 @@ void rgref_fill_normal(float* out, int64_t n) {
 /* Activation::apply (inference/mod.rs:37-53) -> UnaryOp::apply
  * (device/backend.rs:66-78); GELU_C = 0.797_884_6 (backend.rs:61). */
 static float sigmoid_f(float x) { float e = expf(-x); float d = 1.0f + e; return 1.0f / d; }
+/* ReLU = x.max(0.0) (backend.rs:71) as the reference's x86-64 build computes
+ * it.  Rust lowers f32::max to llvm.maxnum, which leaves the sign of an
+ * equal-zero result open; with a constant operand that cannot be NaN, LLVM's
+ * x86 backend emits one maxss with the constant as the source operand
+ * (x > 0 ? x : 0), so NaN and -0.0 both give +0.0. */
+static float rust_relu(float x) { return x > 0.0f ? x : 0.0f; }
 float rgref_act_apply(int act, float p, float x) {
   switch (act) {
     case RGREF_ACT_NONE: return x;
-    case RGREF_ACT_RELU: return fmaxf(x, 0.0f);
+    case RGREF_ACT_RELU: return rust_relu(x);
     case RGREF_ACT_SIGMOID: return sigmoid_f(x);
     case RGREF_ACT_TANH: return tanhf(x);
     case RGREF_ACT_GELU: {

@@ -46,6 +46,12 @@ RG_HD float fmax_nan_ignoring(float a, float b) {
   return a > b ? a : (b > a ? b : a);
 }
 
+// x.max(0.0) as the reference's x86-64 build computes it (backend.rs:71):
+// llvm.maxnum with a constant operand that cannot be NaN becomes one maxss
+// with the constant as its source operand, x > 0 ? x : 0, so NaN and -0.0
+// both give +0.0.
+RG_HD float relu(float x) { return x > 0.0f ? x : 0.0f; }
+
 // fdlibm expm1f.  Branches are kept in the published order; the tanh path
 // only reaches k in {0,-1,-2,-3} (|x|<1) and k in [3,63] (1<=|x|<22).
 RG_HD float expm1f_fdlibm(float x) {
@@ -399,7 +405,7 @@ RG_HD float gelu(float x) {
 
 RG_HD float act_apply(int act, float p, float x) {
   switch (act) {
-    case ACT_RELU: return fmax_nan_ignoring(x, 0.0f);
+    case ACT_RELU: return relu(x);
     case ACT_SIGMOID: return sigmoid(x);
     case ACT_TANH: return tanhf_fast(x);
     case ACT_GELU: return gelu_fast(x);

@@ -787,10 +787,15 @@ static void ensure_capture_buffers(rgnpu_program* P, Plan& plan) {
   plan.capture_ready = true;
 }
 
+static void finalize_profile(rgnpu_program* P);
+
 static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
   if (P->plan && (int)P->plan->in_shape.size() == ndim &&
       std::equal(P->plan->in_shape.begin(), P->plan->in_shape.end(), shape))
     return *P->plan;
+  // A pending profile reads the roles and events of the plan it ran with:
+  // settle it before that plan goes away.
+  if (P->plan && P->profile_pending) finalize_profile(P);
   P->plan.reset();
   P->plan = make_plan(P, shape, ndim);
   return *P->plan;
@@ -800,8 +805,11 @@ static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
 // host waits on [1]); [2 ..] are launch events: the stop event of each kernel
 // the run launches, recorded by that kernel's own dispatch.  Launch events
 // skip the system-scope fence, which is not needed for timing.  A run
-// launches at most one fill plus three kernels per op.
-static size_t launch_event_cap(const rgnpu_program* P) { return 1 + 3 * P->ops.size(); }
+// launches one fill at most plus at most kMaxLaunchesPerOp kernels per op
+// (an FP16 im2col conv with split K launches four: im2col, GEMM, split-K
+// epilogue, NCHW transpose); enqueue() checks the bound.
+static constexpr size_t kMaxLaunchesPerOp = 6;
+static size_t launch_event_cap(const rgnpu_program* P) { return 1 + kMaxLaunchesPerOp * P->ops.size(); }
 static size_t events_per_run(const rgnpu_program* P) { return 2 + launch_event_cap(P); }
 
 static void create_run_event(hipEvent_t* e, size_t index_in_set) {
@@ -1060,6 +1068,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     const int end = launch_events_used();
     plan.roles[i] = {first - 1, pre - 1, end > pre ? end - 1 : pre - 1};
   }
+  if (timed && (size_t)launch_events_used() >= launch_event_cap(P))
+    throw Error(RGNPU_ERR_INVALID, "internal: a run launched more kernels than its event budget");
   // A program with no computing op returns its input (Flatten only).
   bool any = false;
   for (auto& o : P->ops) any |= o->kind != OP_FLATTEN;
@@ -1156,6 +1166,9 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
   RG_HIP(hipSetDevice(device));
   RG_HIP(hipStreamCreateWithFlags(&P->stream, hipStreamNonBlocking));
   try {
+    load_code_object(P->stream);
+    RG_HIP(hipGetLastError());
+    RG_HIP(hipStreamSynchronize(P->stream));
     compile(P.get(), layers, n_layers);
   } catch (...) {
     (void)hipStreamDestroy(P->stream);
@@ -1281,6 +1294,8 @@ int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, in
     P->prof = W->prof;
     P->records = W->records;
     P->have_profile = true;
+    // this completed run supersedes a device run still awaiting its profile
+    P->profile_pending = false;
   }
   RG_API_END
 }

@@ -60,6 +60,8 @@ void set_launch_events(hipEvent_t* events, int cap);
 int launch_events_used();
 
 void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+// Loads the library's kernels on the current device (one empty launch).
+void load_code_object(hipStream_t s);
 // Reads `bytes` (a zero-filled buffer) to displace the memory-side cache.
 void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s);
 

@@ -150,7 +150,10 @@ int rgnpu_rtim_load(const char* path, rgnpu_rtim** out_handle, const rgnpu_layer
           L.kind = RGNPU_LAYER_ACTIVATION;
           const uint32_t code = r.u32();
           L.act_param = r.f32();
-          if (r.ok && code > 6) {
+          // Codes 0..5 only, as save.rs:259-267 reads them: SiLU (code 6 in
+          // this library's enum) has no RTIM code, so a file carrying it is
+          // InvalidData here exactly as it is for the reference.
+          if (r.ok && code > 5) {
             status = RGNPU_ERR_FORMAT;
             err = "unknown activation tag " + std::to_string(code);
           }
@@ -232,6 +235,12 @@ int rgnpu_rtim_save(const char* path, const rgnpu_layer* layers, int64_t n_layer
         break;
       case RGNPU_LAYER_FLATTEN: w.u32(5); break;
       case RGNPU_LAYER_ACTIVATION:
+        // save.rs:209-216 writes codes 0..5; a SiLU layer has none, and a file
+        // holding one could not be read by the reference, so it is refused.
+        if (L.act < RGNPU_ACT_NONE || L.act > RGNPU_ACT_LEAKY_RELU) {
+          status = RGNPU_ERR_INVALID;
+          break;
+        }
         w.u32(6); w.u32((uint32_t)L.act); w.f32(L.act == RGNPU_ACT_LEAKY_RELU ? L.act_param : 0.0f);
         break;
       case RGNPU_LAYER_SOFTMAX: w.u32(7); break;
@@ -242,7 +251,9 @@ int rgnpu_rtim_save(const char* path, const rgnpu_layer* layers, int64_t n_layer
   fclose(f);
   if (status != RGNPU_OK || !w.ok || !flushed) {
     unlink(t.data());
-    rgnpu::g_last_error = status != RGNPU_OK ? "unknown layer kind" : "write failed";
+    rgnpu::g_last_error = status != RGNPU_OK ? "layer has no RTIM encoding (unknown kind, or SiLU, which the "
+                                               "reference format cannot hold)"
+                                             : "write failed";
     return status != RGNPU_OK ? status : RGNPU_ERR_IO;
   }
   if (rename(t.data(), path) != 0) {

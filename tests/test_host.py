@@ -100,7 +100,7 @@ def test_rtim_roundtrip(rg, tmp_path):
     from rustgears_amd.inference import Activation, LayerSpec
     model, _ = configs.cnn(n=2, hw=8, c1=4, c2=8, fc=16)
     layers = model.export() + [LayerSpec.Activation(Activation.leaky_relu(0.25)), LayerSpec.Softmax(),
-                               LayerSpec.Activation(Activation.SILU)]
+                               LayerSpec.Activation(Activation.GELU)]
     p = tmp_path / "m.rtim"
     rg.save_layers(layers, p)
     _layers_equal(layers, rg.load_inference_layers(p))
@@ -117,6 +117,23 @@ def test_rtim_rejects_unknown_activation(rg, tmp_path):
     with pytest.raises(rg.RgnpuError) as e:
         rg.load_inference_layers(p)
     assert e.value.code == 6 and "unknown activation tag 99" in str(e.value)
+
+
+def test_rtim_silu_is_not_interchangeable(rg, tmp_path):
+    # SiLU is this build's extension (layers.rs:341-343 has no export): the
+    # reference reads activation codes 0..5 only (save.rs:259-267), so code 6
+    # is InvalidData on load and a SiLU layer is refused on save.
+    from rustgears_amd.inference import Activation, LayerSpec
+    p = tmp_path / "silu.rtim"
+    p.write_bytes(b"RTIM" + struct.pack("<III", 1, 6, 6) + struct.pack("<f", 0.0))
+    with pytest.raises(rg.RgnpuError) as e:
+        rg.load_inference_layers(p)
+    assert e.value.code == 6 and "unknown activation tag 6" in str(e.value)
+    q = tmp_path / "out.rtim"
+    with pytest.raises(rg.RgnpuError) as e:
+        rg.save_layers([LayerSpec.Activation(Activation.SILU)], q)
+    assert e.value.code == 1 and "SiLU" in str(e.value)
+    assert not q.exists() and not [f for f in os.listdir(tmp_path) if f.startswith(".rtim-")]
 
 
 def test_rtim_rejects_bad_header_tag_and_truncation(rg, tmp_path):
