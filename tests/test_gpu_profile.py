@@ -81,8 +81,10 @@ def test_every_op_timed_with_four_launch_convs(rg, ref):
     for _ in range(2):
         sess.run(x)
         prof = sess.last_npu_profile()
-        assert len(prof.records) == 6
+        assert len(prof.records) == 7
         for r in prof.records:
+            if r.op == "NPU::Flatten":  # a shape change: no kernel
+                continue
             assert r.duration_ns > 0 and r.kernel_ns > 0, r
     sess.close()
 
