@@ -31,7 +31,7 @@ COMMON = [
     "-I", os.path.join(HERE, "..", "include"),
 ]
 
-SOURCES = ["kernels.hip", "program.cpp", "hostcopy.cpp", "rng.cpp", "rtim.cpp"]
+SOURCES = ["kernels.hip", "requant.hip", "program.cpp", "hostcopy.cpp", "rng.cpp", "rtim.cpp"]
 
 
 def _compile(src: str) -> str:
@@ -45,7 +45,7 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

@@ -15,6 +15,7 @@
 #include <charconv>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <array>
@@ -126,6 +127,13 @@ struct OpPlan {
   bool explicit_absmax = true;
   int64_t emit_slot = -1;     // this op's kernel writes absmax into slots[emit_slot..]
   int emit_per_image = 0;
+  // INT8 Linear -> Linear: the producer's GEMM also quantizes the consumer's
+  // input (requant.hip); the consumer then skips its quantize pass.
+  bool requant = false;       // this op's GEMM writes the next Linear's i8 operand
+  int consumer = -1;          // that Linear's op index
+  int64_t sync_base = -1;     // its barrier words in the slot set
+  bool q_ready = false;       // this op's i8 operand was written by its producer
+  int q_in = 0;               // which of the two i8 operand buffers this op's GEMM reads
 };
 
 struct Plan {
@@ -142,6 +150,8 @@ struct Plan {
   int parity = 0;
   int64_t slot_set_words = 0;  // n_slots rounded up to a 128-byte multiple
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
+  DevBuf q_alt;  // second i8 operand buffer: a fused producer writes the one its GEMM does not read
+  int spin_limit = 0;  // requant barrier polls before a workgroup defers (RGNPU_REQUANT_SPIN_LIMIT)
   DevBuf ylo;  // FP16 conv: GEMM output [n*L, O] before the NCHW transpose
   DevBuf ws;  // split-K partial sums
   int64_t ws_bytes = 0;
@@ -735,6 +745,34 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     size_t qb = op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len;
     plan->q_bytes = std::max(plan->q_bytes, qb);
   }
+  // Requantization fused into the producing GEMM: an INT8 Linear on the
+  // unsplit MFMA GEMM whose next computing op is a Linear reading the same
+  // rows (its absmax is this op's emitted slot).  Its barrier words join the
+  // slot set, which every run zeroes.
+  bool any_requant = false;
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
+    const Op& op = *P->ops[i];
+    OpPlan& pl = plan->ops[i];
+    if (op.kind != OP_LINEAR || pl.gemv || op.out_f <= kNarrowMaxN || pl.rows <= 0) continue;
+    if (!gemm_requant_supported(pl.Mpad, op.Npad, op.Kpad)) continue;
+    size_t j = i + 1;
+    while (j < nops && P->ops[j]->kind == OP_FLATTEN) j++;
+    if (j >= nops || P->ops[j]->kind != OP_LINEAR) continue;
+    const Op& cop = *P->ops[j];
+    OpPlan& cpl = plan->ops[j];
+    if (cop.in_f != op.out_f || cpl.rows != pl.rows || cpl.gemv || cpl.explicit_absmax ||
+        pl.emit_slot != cpl.slot_base || cop.Kpad > op.Npad)
+      continue;
+    pl.requant = true;
+    pl.consumer = (int)j;
+    pl.sync_base = round_up(slots, kSpreadStride);
+    slots = pl.sync_base + requant_sync_words(pl.Mpad, op.Npad, op.Kpad);
+    cpl.q_ready = true;
+    cpl.q_in = pl.q_in ^ 1;
+    any_requant = true;
+  }
+  if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
+  else plan->spin_limit = 20000;
   plan->n_slots = slots;
   // The first computing op quantizes the input itself (its absmax is the
   // run's first kernel) unless the input is empty.
@@ -750,6 +788,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   plan->f32[0].ensure(plan->f32_elems * sizeof(float));
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
   plan->q.ensure(plan->q_bytes);
+  if (any_requant) plan->q_alt.ensure(plan->q_bytes);
   if (plan->ylo_elems > 0) plan->ylo.ensure(plan->ylo_elems * sizeof(float));
   if (plan->ws_bytes > 0) plan->ws.ensure((size_t)plan->ws_bytes);
   plan->slot_set_words = round_up(std::max<int64_t>(slots, 1), kSpreadStride);
@@ -941,11 +980,14 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           break;
         }
         uint32_t* slot = slots + pl.slot_base;
-        if (pl.explicit_absmax) {
-          launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s, clear);
-          first_launched();
+        int8_t* const qa = pl.q_in ? plan.q_alt.as<int8_t>() : q;
+        if (!pl.q_ready) {
+          if (pl.explicit_absmax) {
+            launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s, clear);
+            first_launched();
+          }
+          launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base, s);
         }
-        launch_quant_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, q, scales + pl.scale_base, s);
         Epilogue ep;
         ep.bias = op.d_bias.as<float>();
         ep.act = op.act;
@@ -958,15 +1000,26 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
         pre = launch_events_used();
         if (pl.rows > 0) {
-          if (pl.gemv)
-            launch_gemv(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
-          else if (op.out_f <= kNarrowMaxN)
-            launch_gemm_narrow(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Kpad, ep, s);
-          else
-            launch_gemm(q, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
+          if (pl.requant) {
+            const OpPlan& cpl = plan.ops[(size_t)pl.consumer];
+            Requant rq;
+            rq.q = cpl.q_in ? plan.q_alt.as<int8_t>() : q;
+            rq.ldq = P->ops[(size_t)pl.consumer]->Kpad;
+            rq.sync = slots + pl.sync_base;
+            rq.scale_out = scales + cpl.scale_base;
+            rq.keep_f32 = cap ? 1 : 0;
+            rq.spin_limit = plan.spin_limit;
+            launch_gemm_requant(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, rq, s);
+          } else if (pl.gemv) {
+            launch_gemv(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+          } else if (op.out_f <= kNarrowMaxN) {
+            launch_gemm_narrow(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Kpad, ep, s);
+          } else {
+            launch_gemm(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep,
                         plan.ws.as<int32_t>(), plan.ws_bytes, s);
+          }
         }
-        if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
+        if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, qa, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
         break;
       }
       case OP_CONV: {

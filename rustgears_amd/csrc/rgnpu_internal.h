@@ -49,6 +49,21 @@ struct Epilogue {
   int32_t* acc_out = nullptr;          // nullable: i32 accumulator capture
 };
 
+// Requantization fused into a producing Linear's GEMM (requant.hip): the
+// next Linear's i8 operand q [Mpad, ldq] is written by this GEMM once the
+// absmax of its whole output (ep.absmax_out) is known.  sync points at
+// requant_sync_words() zeroed words: [0] arrivals, [1] error flag,
+// [kRequantStateBase + b] the state of workgroup b.
+struct Requant {
+  int8_t* q = nullptr;        // next op's activations [Mpad, ldq], zero padded
+  int64_t ldq = 0;            // next op's Kpad (<= the producer's Npad)
+  uint32_t* sync = nullptr;
+  float* scale_out = nullptr; // nullable: the scale used (capture tap)
+  int keep_f32 = 0;           // also store every f32 output (capture)
+  int spin_limit = 0;         // barrier polls (~1 us each) before a workgroup defers its quantization
+};
+constexpr int64_t kRequantStateBase = 32;
+
 // ---- launchers (kernels.hip) -------------------------------------------
 // Launch events: while set_launch_events(events, cap) is active on this
 // thread, the i-th kernel launched by the launchers below records events[i]
@@ -91,6 +106,24 @@ void launch_gemm(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t
                  int64_t Npad, int64_t Kpad, const Epilogue& ep, int32_t* ws, int64_t ws_bytes,
                  hipStream_t s);
 int64_t gemm_workspace_bytes(int64_t Mpad, int64_t Npad, int64_t Kpad);
+// Tile shape of the large GEMM for a padded problem: 0 = 256 x 256,
+// 1 = 256 x 128, 2 = 128 x 128; splits > 1 when K is split.
+struct GemmChoice {
+  int kind;
+  int splits;
+};
+GemmChoice choose_gemm(int64_t Mpad, int64_t Npad, int64_t Kpad);
+
+// The same GEMM with the next Linear's quantization fused (requant.hip):
+// a persistent grid computes every tile and its fused epilogue, raises
+// ep.absmax_out, meets at a grid barrier, then quantizes its tiles into
+// rq.q with the scale of the whole output.  Only for unsplit problems
+// (choose_gemm(...).splits == 1).  ep.y receives the f32 outputs the
+// quantization reads back (all of them when rq.keep_f32).
+bool gemm_requant_supported(int64_t Mpad, int64_t Npad, int64_t Kpad);
+int64_t requant_sync_words(int64_t Mpad, int64_t Npad, int64_t Kpad);
+void launch_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+                         int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s);
 
 // Same contract for M <= 8 rows (weight-streaming GEMV).
 // INT8 Linear with N <= kNarrowMaxN outputs per row: one wave per row, the

@@ -1,0 +1,110 @@
+"""The next Linear's quantization fused into the producing GEMM (requant.hip).
+
+An INT8 Linear whose next computing op is a Linear quantizes that op's input
+itself: a persistent grid computes its tiles, meets at a grid barrier on the
+per-tensor absmax (npu.rs:312, quantize.rs:18-24), and quantizes its own
+tiles -- the last one from registers, earlier ones from their stored f32
+outputs.  These tests check, bit for bit against the oracle:
+
+* runs without capture (the last tiles' f32 outputs are never written) and
+  with capture (every tap: i8 operand, scale, i32 sums, f32 outputs);
+* workgroups that walk several tiles (more 256 x 256 tiles than CUs), every
+  tile shape, ragged M and N (N not a multiple of 4), activations whose value
+  at 0 is not 0 (the padding columns must not reach the absmax), and chains
+  of three and four fused Linears (the two i8 operand buffers alternate);
+* the deferral path: with RGNPU_REQUANT_SPIN_LIMIT=0 no workgroup waits at
+  the barrier, and the finisher quantizes every other workgroup's tiles;
+* that a fused consumer launches nothing before its GEMM (its op time equals
+  its kernel time in the profile).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact_f32
+from test_gpu_parity import check_against_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _chain(rg, dims, act, seed):
+    from rustgears_amd import nn
+    rg.manual_seed(seed)
+    m = nn.Sequential()
+    for a, b in zip(dims[:-1], dims[1:]):
+        m.add(nn.Linear(a, b))
+        if act is not None:
+            m.add(act())
+    return m.export()
+
+
+def _run_plain(rg, ref, layers, x, what):
+    print(f"[requant] {what} x{tuple(x.shape)}", flush=True)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y = sess.run(x)
+    y2 = sess.run(x)  # a second run on the same plan (slot sets alternate)
+    prof = sess.last_npu_profile()
+    sess.close()
+    want = ref.RefProgram(layers).run(x, parallel=True)
+    assert_bitexact_f32(y, want, what)
+    assert_bitexact_f32(y2, want, what + " (second run)")
+    return prof
+
+
+CASES = [
+    # (name, dims, act, rows): tile shape in the comment (256x256 with > 256
+    # tiles means several tiles per workgroup)
+    ("multi-tile 256x256 gelu", [4000, 4000, 4000], "gelu", 4400),      # 18 x 16 = 288 tiles
+    ("256x128 relu", [1000, 3000, 2000, 500], "relu", 2600),             # 11 x 24 tiles
+    ("128x128 sigmoid ragged n", [700, 1001, 515, 300], "sigmoid", 1500),
+    ("n % 4 != 0 leaky", [333, 257, 259, 17], "leaky", 777),
+    ("four fused tanh", [256, 384, 512, 384, 130], "tanh", 300),
+]
+
+
+def _act(nn, name):
+    return {"gelu": nn.Gelu, "relu": nn.Relu, "sigmoid": nn.Sigmoid, "tanh": nn.Tanh,
+            "leaky": lambda: nn.LeakyRelu(0.03), None: None}[name]
+
+
+@pytest.mark.parametrize("name,dims,act,rows", CASES, ids=[c[0] for c in CASES])
+def test_fused_requant_without_capture(rg, ref, name, dims, act, rows):
+    from rustgears_amd import nn
+    layers = _chain(rg, dims, _act(nn, act), seed=rows + len(dims))
+    x = rg.randn([rows, dims[0]])
+    prof = _run_plain(rg, ref, layers, x, name)
+    gemm_ops = [r for r in prof.records if "Gemm" in r.op]
+    # every Linear after the first reads an operand its producer quantized:
+    # no launch precedes its GEMM inside the op
+    for r in gemm_ops[1:]:
+        assert r.duration_ns == r.kernel_ns, r
+
+
+@pytest.mark.parametrize("name,dims,act,rows", CASES[:3] + CASES[4:], ids=[c[0] for c in CASES[:3] + CASES[4:]])
+def test_fused_requant_capture_taps(rg, ref, name, dims, act, rows):
+    from rustgears_amd import nn
+    layers = _chain(rg, dims, _act(nn, act), seed=rows + len(dims))
+    check_against_oracle(rg, ref, layers, rg.randn([rows, dims[0]]), name)
+
+
+@pytest.mark.parametrize("name,dims,act,rows", [CASES[0], CASES[2], CASES[4]], ids=[CASES[0][0], CASES[2][0],
+                                                                                   CASES[4][0]])
+def test_deferred_quantization_by_the_finisher(rg, ref, monkeypatch, name, dims, act, rows):
+    """No workgroup waits at the barrier: each one that is not last stores its
+    outputs and defers, and the finisher quantizes all of their tiles."""
+    from rustgears_amd import nn
+    monkeypatch.setenv("RGNPU_REQUANT_SPIN_LIMIT", "0")
+    layers = _chain(rg, dims, _act(nn, act), seed=rows + len(dims))
+    x = rg.randn([rows, dims[0]])
+    _run_plain(rg, ref, layers, x, name + " (deferred)")
+    check_against_oracle(rg, ref, layers, x, name + " (deferred, capture)")
+
+
+def test_linear_stack_full_without_capture(rg, ref):
+    """The benchmark config (4 x 4096^2 GELU, 8192 rows) on the fused path,
+    without capture taps, against the oracle's output."""
+    from rustgears_amd import configs
+    model, x = configs.linear_stack()
+    layers = model.export()
+    prof = _run_plain(rg, ref, layers, x, "stack 4096 gelu full (no capture)")
+    for r in prof.records[1:]:
+        assert r.duration_ns == r.kernel_ns, r
