@@ -56,7 +56,10 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {
 // that one-time load (milliseconds) out of the first run and its profile.
 __global__ void load_probe_kernel() {}
 
-void load_code_object(hipStream_t s) { hipLaunchKernelGGL(load_probe_kernel, dim3(1), dim3(64), 0, s); }
+void load_code_object(hipStream_t s) {
+  hipLaunchKernelGGL(load_probe_kernel, dim3(1), dim3(64), 0, s);
+  load_requant_code_object(s);
+}
 
 // Reads n 16-byte words so that the memory-side cache (256 MB on MI355X)
 // holds them instead of whatever a run left there.  The xor of everything

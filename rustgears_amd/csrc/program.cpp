@@ -753,7 +753,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
-    if (op.kind != OP_LINEAR || pl.gemv || op.out_f <= kNarrowMaxN || pl.rows <= 0) continue;
+    if (op.kind != OP_LINEAR || pl.gemv || op.out_f <= kNarrowMaxN || pl.rows <= 0 || op.out_f % 4) continue;
     if (!gemm_requant_supported(pl.Mpad, op.Npad, op.Kpad)) continue;
     size_t j = i + 1;
     while (j < nops && P->ops[j]->kind == OP_FLATTEN) j++;
@@ -772,7 +772,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     any_requant = true;
   }
   if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
-  else plan->spin_limit = 20000;
+  else plan->spin_limit = 100000;  // ~20 ms
   plan->n_slots = slots;
   // The first computing op quantizes the input itself (its absmax is the
   // run's first kernel) unless the input is empty.

@@ -34,25 +34,104 @@
 
 namespace rgnpu {
 
+// Barrier words (u32 offsets into Requant::sync, zeroed before every run):
+// eight group arrival counters and the count of complete groups, each on a
+// 128-byte line of its own; the error flag; one state word per workgroup;
+// and one "go" line per workgroup, written by the finisher and polled by that
+// workgroup alone, so no line is polled by more than one workgroup and no
+// poll competes with the arrivals.
 namespace rqk {
 constexpr uint32_t kOwn = 1, kDeferred = 2;
-constexpr int kFinisherExtraPolls = 20000;  // settle budget of the finisher beyond spin_limit
+constexpr int kGroups = 8;                      // arrival groups: workgroup b joins group b % 8
+constexpr int64_t kLine = 32;                   // u32 words per 128-byte line
+constexpr int64_t kGroupDone = kGroups * kLine; // complete groups
+constexpr int64_t kError = kGroupDone + kLine;  // the finisher saw a workgroup that never settled
+constexpr int64_t kMaxGrid = 1024;              // workgroups of one launch at most
+constexpr int64_t kGoBase = kRequantStateBase + kMaxGrid;
+constexpr int kPollSleep = 8;                   // s_sleep units (64 clocks) between polls
+constexpr int kFinisherExtraPolls = 100000;     // settle budget of the finisher beyond spin_limit
+static_assert(kError < kRequantStateBase, "state words follow the counters");
 }  // namespace rqk
 
-// One wave's (16 FM) x 64 tile of the fused epilogue, staged through the
-// wave's LDS slab 16 rows at a time.  Lane l takes the 4 consecutive columns
-// col0 .. col0 + 3 (col0 = n0 + wn 64 + 4 (l & 15)) of rows 4 p + (l >> 4),
-// p = 0..3, of each slab, so its f32 stores are 16 bytes and its 4 quantized
-// bytes form one word.  The activations are left in acc[i][p] (f32 bits) in
-// that layout.  Returns the max |y| over the valid outputs (NaN ignored, like
-// f32::max); columns past N (zero weights, zero bias) are not outputs.
-template <int ACT, int FM>
-__device__ __forceinline__ float requant_epilogue(int8_t* smem, v4i (&acc)[FM][4], int64_t row0, int64_t col0,
-                                                  int64_t M, int64_t N, float cs, const float4 b4, const Epilogue& ep,
-                                                  bool store, bool vec, int wave, int lane) {
+// The lane layout of the requant epilogue and quantization: lane l of a
+// wave owning rows [wrow0, wrow0 + 16 FM) and columns [wcol0, wcol0 + 64)
+// takes the 4 consecutive columns wcol0 + 4 (l & 15) .. + 3 of rows
+// wrow0 + 16 i + 4 p + (l >> 4), i < FM, p < 4.  N is a multiple of 4 (the
+// plan fuses only then), so a lane's 4 columns are all outputs or all
+// padding.  Which rows are outputs is fixed per lane: 16 i + 4 p < rows_left.
+struct LaneSpan {
+  int32_t rows_left;  // rows of this lane's column group that are outputs, counted from its first row
+  bool cols_ok;       // the lane's 4 columns are outputs (< N)
+};
+
+__device__ __forceinline__ LaneSpan lane_span(int32_t wrow0, int32_t wcol0, int32_t M, int32_t N, int lane) {
+  LaneSpan s;
+  const int32_t rl = M - wrow0 - (lane >> 4);
+  s.rows_left = rl < 0 ? 0 : rl;
+  s.cols_ok = wcol0 + 4 * (lane & 15) < N;
+  return s;
+}
+
+// quantize_one (quantize.rs:22) without branches: v * inv rounded half away
+// from zero (trunc, then +-1 when the dropped fraction is at least 0.5; the
+// fraction x - trunc(x) is exact), converted by the hardware's saturating
+// v_cvt_i32_f32 (NaN -> 0, +-inf and out-of-range values -> +-(2^31 - 1)),
+// then clamped to +-127 as an integer.  The rounded value is an integer, so
+// clamping before or after the conversion agrees: the result equals
+// round, clamp(-127, 127), `as i8` for every input, NaN and infinities
+// included.
+__device__ __forceinline__ int32_t q8(float v, float inv) {
+  const float r = __builtin_roundf(v * inv);
+  int32_t i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(r));
+  return i < -127 ? -127 : (i > 127 ? 127 : i);
+}
+
+// Four quantized bytes of one row, little-endian by column.
+__device__ __forceinline__ uint32_t q8x4(v4f v, float inv) {
+  const uint32_t b0 = (uint32_t)q8(v[0], inv), b1 = (uint32_t)q8(v[1], inv);
+  const uint32_t b2 = (uint32_t)q8(v[2], inv), b3 = (uint32_t)q8(v[3], inv);
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // bytes b0.0, b1.0
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Masked stores without branches: raw buffer stores over a wave-uniform
+// base with a record limit of 2^31 bytes; an element outside the output gets
+// the per-lane offset 2^31, which the hardware's bounds check drops, and the
+// row offset travels in the scalar offset.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+constexpr uint32_t kDropOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kDropOffset, 0x00020000);
+}
+
+// Quantizes 4 values into q's row (byte offset qoff from the wave's q base):
+// rows past M and columns past N are the operand's zero padding.
+__device__ __forceinline__ void quant_store(__amdgpu_buffer_rsrc_t rq, v4f v, float inv, uint32_t qoff, uint32_t soff,
+                                            bool row_ok, bool cols_ok, bool q_ok) {
+  const uint32_t w = row_ok && cols_ok ? q8x4(v, inv) : 0u;
+  __builtin_amdgcn_raw_buffer_store_b32(w, rq, (int)(q_ok ? qoff : kDropOffset), (int)soff, 0);
+}
+
+// One wave's (16 FM) x 64 tile of the fused epilogue (quantize.rs:109-111),
+// staged through the wave's LDS slab 16 rows at a time and read back in the
+// lane layout above, so the f32 stores (when `store`) are 16 bytes.  The
+// activations are left in acc[i][p] (f32 bits); with CAP the i32 sums are
+// stored too.  Returns the max |y| over the outputs (NaN ignored, like
+// f32::max); padding columns (zero weights and bias) are not outputs.
+template <int ACT, int FM, bool CAP>
+__device__ __forceinline__ float requant_epilogue(int8_t* smem, v4i (&acc)[FM][4], int32_t wrow0, int32_t wcol0,
+                                                  int32_t N, const LaneSpan& sp, float cs, const float4 b4,
+                                                  const Epilogue& ep, bool store, int wave, int lane) {
   int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
   const int sub = lane >> 4, c4 = (lane & 15) * 4;
   const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+  const int64_t base = (int64_t)wrow0 * N + wcol0;
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + base);
+  const uint32_t voff = (uint32_t)((sub * N + c4) * 4);
+  const uint32_t row_bytes = (uint32_t)N * 4u;
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < FM; i++) {
@@ -62,32 +141,22 @@ __device__ __forceinline__ float requant_epilogue(int8_t* smem, v4i (&acc)[FM][4
       for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      const int rr = p * 4 + sub;
+      const int rr = p * 4 + sub, ro = i * 16 + p * 4;
       const v4i a = *reinterpret_cast<const v4i*>(slab + rr * big::SLAB_LD + c4);
-      const int64_t row = row0 + i * 16 + rr;
       v4f v;
 #pragma unroll
       for (int c = 0; c < 4; c++) v[c] = epi_value<ACT>(a[c], cs, bb[c], ep.act_param);
-      if (row < M) {
-        float* yr = ep.y + row * N + col0;
-        if (vec && col0 + 4 <= N) {
-          if (store) *reinterpret_cast<v4f*>(yr) = v;
-#pragma unroll
-          for (int c = 0; c < 4; c++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[c]));
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; c++)
-            if (col0 + c < N) {
-              if (store) yr[c] = v[c];
-              amax = __builtin_fmaxf(amax, __builtin_fabsf(v[c]));
-            }
-        }
-        if (ep.acc_out) {
-#pragma unroll
-          for (int c = 0; c < 4; c++)
-            if (col0 + c < N) ep.acc_out[row * N + col0 + c] = a[c];
-        }
-      }
+      const bool ok = ro < sp.rows_left && sp.cols_ok;
+      const float m4 = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1])),
+                                       __builtin_fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
+      amax = __builtin_fmaxf(amax, ok ? m4 : 0.0f);
+      const uint32_t soff = (uint32_t)ro * row_bytes;
+      if (store || CAP)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), ry, (int)(ok ? voff : kDropOffset),
+                                               (int)soff, 0);
+      if constexpr (CAP)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, a), bounded_rsrc(ep.acc_out + base),
+                                               (int)(ok ? voff : kDropOffset), (int)soff, 0);
       acc[i][p] = __builtin_bit_cast(v4i, v);
     }
   }
@@ -97,228 +166,260 @@ __device__ __forceinline__ float requant_epilogue(int8_t* smem, v4i (&acc)[FM][4
 // Stores the activations requant_epilogue left in acc as f32 (a workgroup
 // that defers its quantization leaves them for the finisher).
 template <int FM>
-__device__ __forceinline__ void store_kept_f32(const v4i (&acc)[FM][4], float* y, int64_t row0, int64_t col0,
-                                               int64_t M, int64_t N, bool vec, int lane) {
-  const int sub = lane >> 4;
+__device__ __forceinline__ void store_kept_f32(const v4i (&acc)[FM][4], float* y, int32_t wrow0, int32_t wcol0,
+                                               int32_t N, const LaneSpan& sp, int lane) {
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)wrow0 * N + wcol0);
+  const uint32_t voff = (uint32_t)(((lane >> 4) * N + 4 * (lane & 15)) * 4);
 #pragma unroll
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      const int64_t row = row0 + i * 16 + p * 4 + sub;
-      if (row >= M) continue;
-      const v4f v = __builtin_bit_cast(v4f, acc[i][p]);
-      float* yr = y + row * N + col0;
-      if (vec && col0 + 4 <= N) {
-        *reinterpret_cast<v4f*>(yr) = v;
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-          if (col0 + c < N) yr[c] = v[c];
-      }
+      const int ro = i * 16 + p * 4;
+      const bool ok = ro < sp.rows_left && sp.cols_ok;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, acc[i][p]), ry, (int)(ok ? voff : kDropOffset),
+                                             (int)((uint32_t)ro * (uint32_t)N * 4u), 0);
     }
 }
 
-// Four quantized bytes of row `row`, columns col0 .. col0 + 3; positions
-// outside [0, M) x [0, N) are the zero padding of the next operand.
-__device__ __forceinline__ uint32_t quant_word(v4f v, int64_t row, int64_t col0, int64_t M, int64_t N, float inv) {
-  uint32_t w = 0;
-  if (row < M) {
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (col0 + c < N) w |= (uint32_t)(uint8_t)rgmath::quantize_one(v[c], inv) << (8 * c);
-  }
-  return w;
-}
-
-// Quantizes the activations kept in acc (requant_epilogue layout) into
-// q [.., ldq].  Columns at or past ldq (the producer's Npad may exceed the
-// consumer's Kpad) are not part of the operand.
+// Quantizes the activations kept in acc into q [.., ldq]: every row of the
+// wave's part is written (zero rows past M and zero columns past N are the
+// operand's padding); columns at or past ldq (the producer's Npad may exceed
+// the consumer's Kpad) are not part of the operand.
 template <int FM>
-__device__ __forceinline__ void quantize_kept(const v4i (&acc)[FM][4], int8_t* q, int64_t ldq, int64_t row0,
-                                              int64_t col0, int64_t M, int64_t N, float inv, int lane) {
-  if (col0 >= ldq) return;
-  const int sub = lane >> 4;
+__device__ __forceinline__ void quantize_kept(const v4i (&acc)[FM][4], int8_t* q, int32_t ldq, int32_t wrow0,
+                                              int32_t wcol0, const LaneSpan& sp, float inv, int lane) {
+  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)wrow0 * ldq + wcol0);
+  const uint32_t qoff = (uint32_t)((lane >> 4) * ldq + 4 * (lane & 15));
+  const bool q_ok = wcol0 + 4 * (lane & 15) < ldq;
 #pragma unroll
   for (int i = 0; i < FM; i++)
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-      const int64_t row = row0 + i * 16 + p * 4 + sub;
-      *reinterpret_cast<uint32_t*>(q + row * ldq + col0) =
-          quant_word(__builtin_bit_cast(v4f, acc[i][p]), row, col0, M, N, inv);
+      const int ro = i * 16 + p * 4;
+      quant_store(rq, __builtin_bit_cast(v4f, acc[i][p]), inv, qoff, (uint32_t)ro * (uint32_t)ldq, ro < sp.rows_left,
+                  sp.cols_ok, q_ok);
     }
 }
 
 // Quantizes one wave's (16 FM) x 64 part of a tile from its stored f32
-// outputs, in the same lane layout.
+// outputs, 4 slabs (16 loads per lane) in flight at a time.  Buffer loads
+// with the row offset in a scalar: no address registers per load.
 template <int FM>
-__device__ __forceinline__ void quantize_stored(const float* y, int8_t* q, int64_t ldq, int64_t row0, int64_t col0,
-                                                int64_t M, int64_t N, float inv, bool vec, int lane) {
-  if (col0 >= ldq) return;
-  const int sub = lane >> 4;
+__device__ __forceinline__ void quantize_stored(const float* y, int8_t* q, int32_t ldq, int32_t wrow0, int32_t wcol0,
+                                                int32_t N, const LaneSpan& sp, float inv, int lane) {
+  constexpr int BATCH = FM < 4 ? FM : 4;
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)wrow0 * N + wcol0);
+  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)wrow0 * ldq + wcol0);
+  const uint32_t voff = (uint32_t)(((lane >> 4) * N + 4 * (lane & 15)) * 4);
+  const uint32_t qoff = (uint32_t)((lane >> 4) * ldq + 4 * (lane & 15));
+  const bool q_ok = wcol0 + 4 * (lane & 15) < ldq;
+  const uint32_t row_bytes = (uint32_t)N * 4u;
 #pragma unroll
-  for (int i = 0; i < FM; i++) {
-    v4f v[4];
+  for (int i0 = 0; i0 < FM; i0 += BATCH) {
+    v4f v[BATCH][4];
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const int64_t row = row0 + i * 16 + p * 4 + sub;
-      v[p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      if (row < M) {
-        const float* yr = y + row * N + col0;
-        if (vec && col0 + 4 <= N) {
-          v[p] = *reinterpret_cast<const v4f*>(yr);
-        } else {
+    for (int i = 0; i < BATCH; i++)
 #pragma unroll
-          for (int c = 0; c < 4; c++)
-            if (col0 + c < N) v[p][c] = yr[c];
-        }
+      for (int p = 0; p < 4; p++) {
+        const int ro = (i0 + i) * 16 + p * 4;
+        const bool ok = ro < sp.rows_left && sp.cols_ok;
+        v[i][p] = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)(ok ? voff : kDropOffset), (int)(ro * row_bytes), 0));
       }
-    }
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const int64_t row = row0 + i * 16 + p * 4 + sub;
-      *reinterpret_cast<uint32_t*>(q + row * ldq + col0) = quant_word(v[p], row, col0, M, N, inv);
-    }
+    for (int i = 0; i < BATCH; i++)
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int ro = (i0 + i) * 16 + p * 4;
+        quant_store(rq, v[i][p], inv, qoff, (uint32_t)ro * (uint32_t)ldq, ro < sp.rows_left, sp.cols_ok, q_ok);
+      }
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT>
+// Per-launch constants of the fused kernel, 32-bit where the plan bounds
+// them (the fused path requires N % 4 == 0 and 128 N * 4 < 2^31).
+struct RequantShape {
+  int32_t M, N, ldq, nk, tiles_m, tiles_n;
+};
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kernel(
-    const int8_t* __restrict__ A, const int8_t* __restrict__ B, int64_t M, int64_t N, int64_t Kpad, int tiles_m,
-    int tiles_n, Epilogue ep, Requant rq) {
+    const int8_t* __restrict__ A, const int8_t* __restrict__ B, RequantShape sh, Epilogue ep, Requant rq) {
   using namespace big;
   constexpr int NW = WAVES_M * WAVES_N;
   static_assert(BM == 16 * FM * WAVES_M && BN == 64 * WAVES_N, "wave tile is (16 FM) x 64");
   constexpr int ST = (BM + BN) * BK;
   static_assert(NW * SLAB <= STAGES * ST, "epilogue slabs reuse the ring");
-  __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST];
-  __shared__ uint32_t s_flag, s_ndef;
+  // One LDS array only, the few words of block state at its end: with a
+  // second __shared__ variable the compiler no longer tells the ring's DMA
+  // writes (global_load_lds) apart from the K loop's LDS reads and waits for
+  // every outstanding load (vmcnt(0)) in each K step, serializing the ring.
+  __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST + 64];
+  uint32_t* const blk = reinterpret_cast<uint32_t*>(smem + STAGES * ST);  // [0] flag, [1] deferred, [2..] wave maxima
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int T = tiles_m * tiles_n, G = (int)gridDim.x, b = (int)blockIdx.x;
+  const int T = sh.tiles_m * sh.tiles_n, G = (int)gridDim.x, b = (int)blockIdx.x;
   const int ntile = (T - b + G - 1) / G;  // >= 1: the grid never exceeds the tile count
-  const int nk = (int)(Kpad / BK);
-  const int64_t wrow = (int64_t)wm * 16 * FM, wcol = (int64_t)wn * 64 + 4 * (lane & 15);
-  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(ep.y) & 15) == 0;
+  const int32_t M = sh.M, N = sh.N, wrow = wm * 16 * FM, wcolw = wn * 64;
   // partial of the input absmax, folded after the first K loop
   const uint32_t absmax_part = tensor_absmax_part(ep.absmax_in);
   float cs = 0.0f, amax = 0.0f;
-  int64_t m0 = 0, n0 = 0;
+  int32_t m0 = 0, n0 = 0;
   v4i acc[FM][4];
   for (int it = 0; it < ntile; it++) {
     int tm, tn;
-    tile_coords(b + it * G, tiles_m, tiles_n, tm, tn);
-    m0 = (int64_t)tm * BM;
-    n0 = (int64_t)tn * BN;
-    const float4 b4 = *reinterpret_cast<const float4*>(ep.bias + n0 + wcol);  // bias is padded to Npad
+    tile_coords(b + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
+    m0 = tm * BM;
+    n0 = tn * BN;
     if (it > 0) {
-      // the previous epilogue's slabs live in the ring the K loop refills
+      // the previous epilogue's slabs live in the ring the K loop refills;
+      // its stores are drained once here rather than left to the K loop
+      wait_vmcnt<0>();
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
     }
-    big_kloop<BM, BN, WAVES_M, WAVES_N, STAGES, FM, kModeI8>(smem, A, B, Kpad, m0, n0, 0, nk, wave, wm, wn, lane,
-                                                             acc);
+    const float4 b4 = *reinterpret_cast<const float4*>(ep.bias + n0 + wcolw + 4 * (lane & 15));  // padded to Npad
+    big_kloop<BM, BN, WAVES_M, WAVES_N, STAGES, FM, kModeI8>(smem, A, B, (int64_t)sh.nk * BK, m0, n0, 0, sh.nk, wave,
+                                                             wm, wn, lane, acc);
     if (it == 0) cs = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
-    const bool store = it + 1 < ntile || rq.keep_f32;
-    const float t = requant_epilogue<ACT, FM>(smem, acc, m0 + wrow, n0 + wcol, M, N, cs, b4, ep, store, vec, wave,
-                                              lane);
+    const LaneSpan sp = lane_span(m0 + wrow, n0 + wcolw, M, N, lane);
+    const float t = requant_epilogue<ACT, FM, CAP>(smem, acc, m0 + wrow, n0 + wcolw, N, sp, cs, b4, ep,
+                                                   it + 1 < ntile || rq.keep_f32, wave, lane);
     amax = __builtin_fmaxf(amax, t);
   }
 
-  // Publish this workgroup's absmax, then arrive.  The release fence orders
-  // the absmax atomics and the f32 stores above before the arrival.
+  // Publish this workgroup's absmax (one atomic), then arrive.  Everything
+  // crossing workgroups on this path is a device-scope atomic (the absmax
+  // partials, the arrival counts, the go lines, the states), performed where
+  // all XCDs see it; the atomic has completed before the arrival (vmcnt
+  // counts atomics without return on gfx9), and a workgroup reads back only
+  // its own f32 stores.  No cache writeback or invalidation is needed, so
+  // none is done: agent-scope fences here would flush the L2 of an XCD for
+  // every wave.
   {
     const uint32_t m = wave_max_u32(rgmath::fbits(amax));
-    if (lane == 0) spread_max(ep.absmax_out, m);
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(rq.sync, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t flag = prev + 1 == (uint32_t)G ? 2u : 0u;  // 2: this arrival completed the barrier
-    for (int k = 0; flag == 0 && k < rq.spin_limit; k++) {
-      __builtin_amdgcn_s_sleep(32);
-      if (__hip_atomic_load(rq.sync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= (uint32_t)G) flag = 1;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // the epilogue slabs are done with
+    if (lane == 0) blk[2 + wave] = m;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (tid == 0) {
+      uint32_t r = blk[2];
+      for (int w = 1; w < NW; w++) r = blk[2 + w] > r ? blk[2 + w] : r;
+      if (r) atomicMax(ep.absmax_out + (b & (kSpread - 1)) * kSpreadStride, r);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the atomic has completed before the arrival
     }
-    s_flag = flag;
+  }
+  __builtin_amdgcn_s_barrier();
+  if (tid == 0) {
+    // two-level arrival: the last of a group counts the group, the arrival
+    // that completes the last group is the finisher
+    const int g = b % rqk::kGroups;
+    const uint32_t in_group = (uint32_t)((G - g + rqk::kGroups - 1) / rqk::kGroups);
+    const uint32_t groups = (uint32_t)(G < rqk::kGroups ? G : rqk::kGroups);
+    uint32_t flag = 0;
+    if (__hip_atomic_fetch_add(rq.sync + g * rqk::kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            in_group &&
+        __hip_atomic_fetch_add(rq.sync + rqk::kGroupDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            groups)
+      flag = 2;
+    uint32_t* const go = rq.sync + rqk::kGoBase + (int64_t)b * rqk::kLine;
+    for (int k = 0; flag == 0 && k < rq.spin_limit; k++) {
+      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
+      if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) flag = 1;
+    }
+    blk[0] = flag;
   }
   __syncthreads();
-  const uint32_t flag = s_flag;
+  const uint32_t flag = blk[0];
+  if (flag == 2) {
+    // release every other workgroup: one line each
+    for (int w = tid; w < G; w += blockDim.x)
+      if (w != b)
+        __hip_atomic_store(rq.sync + rqk::kGoBase + (int64_t)w * rqk::kLine, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const LaneSpan sp_last = lane_span(m0 + wrow, n0 + wcolw, M, N, lane);
   if (flag == 0) {
-    // Waited too long: the finisher quantizes this workgroup's tiles.
-    if (!rq.keep_f32) store_kept_f32<FM>(acc, ep.y, m0 + wrow, n0 + wcol, M, N, vec, lane);
+    // Waited too long: the finisher quantizes this workgroup's tiles from the
+    // f32 outputs, which it reads from another XCD -- so here, and only on
+    // this path, a release fence writes them back before the state says so.
+    if (!rq.keep_f32 && !CAP) store_kept_f32<FM>(acc, ep.y, m0 + wrow, n0 + wcolw, N, sp_last, lane);
     __threadfence();
     __syncthreads();
     if (tid == 0)
       __hip_atomic_store(rq.sync + kRequantStateBase + b, rqk::kDeferred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  __threadfence();  // acquire: every workgroup's absmax partials and stores
   if (tid == 0)
     __hip_atomic_store(rq.sync + kRequantStateBase + b, rqk::kOwn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t part =
       __hip_atomic_load(ep.absmax_out + lane * kSpreadStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float scale = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
   const float inv = 1.0f / scale;
-  // earlier tiles from their stored outputs, the last one from registers
+  // the last tile from registers, then the earlier tiles from their stored outputs
+  quantize_kept<FM>(acc, rq.q, sh.ldq, m0 + wrow, n0 + wcolw, sp_last, inv, lane);
+  __builtin_amdgcn_sched_barrier(0);
   for (int it = 0; it + 1 < ntile; it++) {
     int tm, tn;
-    tile_coords(b + it * G, tiles_m, tiles_n, tm, tn);
-    quantize_stored<FM>(ep.y, rq.q, rq.ldq, (int64_t)tm * BM + wrow, (int64_t)tn * BN + wcol, M, N, inv, vec, lane);
+    tile_coords(b + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
+    const int32_t r0 = tm * BM + wrow, c0 = tn * BN + wcolw;
+    quantize_stored<FM>(ep.y, rq.q, sh.ldq, r0, c0, N, lane_span(r0, c0, M, N, lane), inv, lane);
   }
-  quantize_kept<FM>(acc, rq.q, rq.ldq, m0 + wrow, n0 + wcol, M, N, inv, lane);
   if (flag != 2) return;
 
   // Finisher: the scale tap, then the tiles of every deferred workgroup.
   if (tid == 0 && rq.scale_out) *rq.scale_out = scale;
   uint32_t* list = reinterpret_cast<uint32_t*>(smem);  // the ring is free: no K loop follows
-  if (tid == 0) s_ndef = 0;
+  if (tid == 0) blk[1] = 0;
   __syncthreads();
   for (int w = tid; w < G; w += blockDim.x) {
     uint32_t st = 0;
     for (int k = 0; k < rq.spin_limit + rqk::kFinisherExtraPolls; k++) {
       st = __hip_atomic_load(rq.sync + kRequantStateBase + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (st != 0) break;
-      __builtin_amdgcn_s_sleep(32);
+      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
     }
-    if (st == 0) __hip_atomic_store(rq.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (st == rqk::kDeferred) list[atomicAdd(&s_ndef, 1u)] = (uint32_t)w;
+    if (st == 0) __hip_atomic_store(rq.sync + rqk::kError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (st == rqk::kDeferred) list[atomicAdd(&blk[1], 1u)] = (uint32_t)w;
   }
-  __threadfence();  // acquire: the deferred workgroups' stored outputs
   __syncthreads();
-  const int ndef = (int)s_ndef;
+  const int ndef = (int)blk[1];
+  if (ndef > 0) __threadfence();  // acquire: the deferred workgroups' stored outputs
   for (int d = 0; d < ndef; d++) {
     const int w = (int)list[d];
     const int wt = (T - w + G - 1) / G;
     for (int it = 0; it < wt; it++) {
       int tm, tn;
-      tile_coords(w + it * G, tiles_m, tiles_n, tm, tn);
-      quantize_stored<FM>(ep.y, rq.q, rq.ldq, (int64_t)tm * BM + wrow, (int64_t)tn * BN + wcol, M, N, inv, vec,
-                          lane);
+      tile_coords(w + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
+      const int32_t r0 = tm * BM + wrow, c0 = tn * BN + wcolw;
+      quantize_stored<FM>(ep.y, rq.q, sh.ldq, r0, c0, N, lane_span(r0, c0, M, N, lane), inv, lane);
     }
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT>
-static void launch_requant_act(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP>
+static void launch_requant_act(const int8_t* A, const int8_t* B, const RequantShape& sh, int64_t Mpad, int64_t Npad,
                                int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s) {
   constexpr int threads = WAVES_M * WAVES_N * 64;
-  const void* fn = reinterpret_cast<const void*>(&gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT>);
+  const void* fn =
+      reinterpret_cast<const void*>(&gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP>);
   static const int64_t cap = resident_blocks(fn, threads);
-  const int tm = (int)(Mpad / BM), tn = (int)(Npad / BN);
-  const int64_t T = (int64_t)tm * tn;
-  const int64_t G = T < cap ? T : cap;
-  if (G > requant_sync_words(Mpad, Npad, Kpad) - kRequantStateBase)
+  const int64_t T = (int64_t)sh.tiles_m * sh.tiles_n;
+  int64_t G = T < cap ? T : cap;
+  if (G > rqk::kMaxGrid) G = rqk::kMaxGrid;
+  if (rqk::kGoBase + G * rqk::kLine > requant_sync_words(Mpad, Npad, Kpad))
     throw std::logic_error("requant: more workgroups than sync words");
-  RG_LAUNCH((gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT>), dim3((unsigned)G), dim3(threads), 0,
-            s, A, B, M, N, Kpad, tm, tn, ep, rq);
+  RG_LAUNCH((gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP>), dim3((unsigned)G),
+            dim3(threads), 0, s, A, B, sh, ep, rq);
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM>
-static void launch_requant_shape(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, bool CAP>
+static void launch_requant_shape(const int8_t* A, const int8_t* B, const RequantShape& sh, int64_t Mpad, int64_t Npad,
                                  int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s) {
 #define RG_RQ(ACTV) \
-  launch_requant_act<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACTV>(A, B, M, N, Mpad, Npad, Kpad, ep, rq, s)
+  launch_requant_act<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACTV, CAP>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s)
   switch (ep.act) {
     case rgmath::ACT_RELU: RG_RQ(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: RG_RQ(rgmath::ACT_SIGMOID); break;
@@ -331,33 +432,53 @@ static void launch_requant_shape(const int8_t* A, const int8_t* B, int64_t M, in
 #undef RG_RQ
 }
 
+// This translation unit is its own code object: loaded at program creation
+// with the rest (see load_code_object).
+__global__ void requant_load_probe_kernel() {}
+
+void load_requant_code_object(hipStream_t s) {
+  hipLaunchKernelGGL(requant_load_probe_kernel, dim3(1), dim3(64), 0, s);
+}
+
 bool gemm_requant_supported(int64_t Mpad, int64_t Npad, int64_t Kpad) {
   if (Kpad % big::BK || Mpad % 128 || Npad % 128 || Kpad <= 0) return false;
+  // 32-bit offsets: whole rows and 128-row spans of the f32 output and of q
+  if (Mpad * Npad * 4 >= ((int64_t)1 << 31) * 64 || Npad * 4 * 128 >= ((int64_t)1 << 31)) return false;
   return choose_gemm(Mpad, Npad, Kpad).splits == 1;
 }
 
 int64_t requant_sync_words(int64_t Mpad, int64_t Npad, int64_t Kpad) {
-  // the grid never exceeds the tile count or two workgroups per CU of 256
+  // the grid never exceeds the tile count or kMaxGrid
   const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
   const int64_t bm = g.kind == 2 ? 128 : 256, bn = g.kind == 0 ? 256 : 128;
   int64_t T = (Mpad / bm) * (Npad / bn);
-  if (T > 4096) T = 4096;
-  return round_up(kRequantStateBase + T, 32);
+  if (T > rqk::kMaxGrid) T = rqk::kMaxGrid;
+  return rqk::kGoBase + T * rqk::kLine;
 }
 
 void launch_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                          int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s) {
-  if (!gemm_requant_supported(Mpad, Npad, Kpad)) throw std::logic_error("requant: the GEMM must be unsplit");
-  if (!ep.absmax_out || !rq.q || !rq.sync || rq.ldq <= 0 || rq.ldq > Npad || rq.ldq % 16)
-    throw std::logic_error("requant: absmax slot, operand and sync words are required");
+  if (!gemm_requant_supported(Mpad, Npad, Kpad) || N % 4 || M >= ((int64_t)1 << 31))
+    throw std::logic_error("requant: the GEMM must be unsplit and N a multiple of 4");
+  if (!ep.absmax_out || !rq.q || !rq.sync || rq.ldq <= 0 || rq.ldq > Npad || rq.ldq % 16 ||
+      (reinterpret_cast<uintptr_t>(ep.y) & 15) || (reinterpret_cast<uintptr_t>(rq.q) & 15))
+    throw std::logic_error("requant: absmax slot, aligned operand and output, and sync words are required");
   if (M <= 0) return;
   const GemmChoice g = choose_gemm(Mpad, Npad, Kpad);
-  if (g.kind == 0)
-    launch_requant_shape<256, 256, 2, 4, 4, 1, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, rq, s);
-  else if (g.kind == 1)
-    launch_requant_shape<256, 128, 2, 2, 3, 2, 8>(A, B, M, N, Mpad, Npad, Kpad, ep, rq, s);
-  else
-    launch_requant_shape<128, 128, 2, 2, 4, 2, 4>(A, B, M, N, Mpad, Npad, Kpad, ep, rq, s);
+  const int64_t bm = g.kind == 2 ? 128 : 256, bn = g.kind == 0 ? 256 : 128;
+  const RequantShape sh{(int32_t)M, (int32_t)N, (int32_t)rq.ldq, (int32_t)(Kpad / big::BK), (int32_t)(Mpad / bm),
+                        (int32_t)(Npad / bn)};
+  const bool cap = ep.acc_out != nullptr;
+  if (g.kind == 0) {
+    cap ? launch_requant_shape<256, 256, 2, 4, 4, 1, 8, true>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s)
+        : launch_requant_shape<256, 256, 2, 4, 4, 1, 8, false>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s);
+  } else if (g.kind == 1) {
+    cap ? launch_requant_shape<256, 128, 2, 2, 3, 2, 8, true>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s)
+        : launch_requant_shape<256, 128, 2, 2, 3, 2, 8, false>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s);
+  } else {
+    cap ? launch_requant_shape<128, 128, 2, 2, 4, 2, 4, true>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s)
+        : launch_requant_shape<128, 128, 2, 2, 4, 2, 4, false>(A, B, sh, Mpad, Npad, Kpad, ep, rq, s);
+  }
 }
 
 }  // namespace rgnpu

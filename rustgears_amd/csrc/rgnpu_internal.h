@@ -52,17 +52,17 @@ struct Epilogue {
 // Requantization fused into a producing Linear's GEMM (requant.hip): the
 // next Linear's i8 operand q [Mpad, ldq] is written by this GEMM once the
 // absmax of its whole output (ep.absmax_out) is known.  sync points at
-// requant_sync_words() zeroed words: [0] arrivals, [1] error flag,
-// [kRequantStateBase + b] the state of workgroup b.
+// requant_sync_words() zeroed words (arrival counters, per-workgroup states
+// from kRequantStateBase on, and per-workgroup release lines).
 struct Requant {
   int8_t* q = nullptr;        // next op's activations [Mpad, ldq], zero padded
   int64_t ldq = 0;            // next op's Kpad (<= the producer's Npad)
   uint32_t* sync = nullptr;
   float* scale_out = nullptr; // nullable: the scale used (capture tap)
   int keep_f32 = 0;           // also store every f32 output (capture)
-  int spin_limit = 0;         // barrier polls (~1 us each) before a workgroup defers its quantization
+  int spin_limit = 0;         // barrier polls (~0.2 us each) before a workgroup defers its quantization
 };
-constexpr int64_t kRequantStateBase = 32;
+constexpr int64_t kRequantStateBase = 320;
 
 // ---- launchers (kernels.hip) -------------------------------------------
 // Launch events: while set_launch_events(events, cap) is active on this
@@ -75,8 +75,10 @@ void set_launch_events(hipEvent_t* events, int cap);
 int launch_events_used();
 
 void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
-// Loads the library's kernels on the current device (one empty launch).
+// Loads the library's kernels on the current device (one empty launch per
+// code object: kernels.hip and requant.hip).
 void load_code_object(hipStream_t s);
+void load_requant_code_object(hipStream_t s);
 // Reads `bytes` (a zero-filled buffer) to displace the memory-side cache.
 void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s);
 

@@ -9,7 +9,8 @@ outputs.  These tests check, bit for bit against the oracle:
 * runs without capture (the last tiles' f32 outputs are never written) and
   with capture (every tap: i8 operand, scale, i32 sums, f32 outputs);
 * workgroups that walk several tiles (more 256 x 256 tiles than CUs), every
-  tile shape, ragged M and N (N not a multiple of 4), activations whose value
+  tile shape, ragged M and N (padding columns within a tile; an N that is not
+  a multiple of 4 keeps the separate quantize pass), activations whose value
   at 0 is not 0 (the padding columns must not reach the absmax), and chains
   of three and four fused Linears (the two i8 operand buffers alternate);
 * the deferral path: with RGNPU_REQUANT_SPIN_LIMIT=0 no workgroup waits at
@@ -37,6 +38,35 @@ def _chain(rg, dims, act, seed):
     return m.export()
 
 
+def _rup(v, m):
+    return (v + m - 1) // m * m
+
+
+def _unsplit(mpad, npad, kpad):
+    """The large GEMM's choice (kernels.hip choose_gemm): False when K is split."""
+    if mpad % 256 == 0 and npad % 256 == 0 and (mpad // 256) * (npad // 256) >= 256:
+        return True
+    if mpad % 256 == 0 and npad % 128 == 0 and (mpad // 256) * (npad // 128) >= 256:
+        return True
+    tiles, nk = (mpad // 128) * (npad // 128), kpad // 64
+    if tiles >= 128:
+        return True
+    s = max(1, min(512 // max(tiles, 1), nk // 4))
+    ks = -(-nk // s)
+    return -(-nk // ks) == 1
+
+
+def _expected_fused(dims, rows):
+    """Per Linear after the first: is its input quantized by its producer?
+    (producer on the unsplit MFMA GEMM -- more than 8 rows, more than 16
+    outputs -- with a multiple of 4 outputs)"""
+    mpad = _rup(rows, 256)
+    out = []
+    for k, n, n2 in zip(dims[:-2], dims[1:-1], dims[2:]):
+        out.append(rows > 8 and n > 16 and n % 4 == 0 and _unsplit(mpad, _rup(n, 256), _rup(k, 128)))
+    return out
+
+
 def _run_plain(rg, ref, layers, x, what):
     print(f"[requant] {what} x{tuple(x.shape)}", flush=True)
     sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
@@ -55,8 +85,8 @@ CASES = [
     # tiles means several tiles per workgroup)
     ("multi-tile 256x256 gelu", [4000, 4000, 4000], "gelu", 4400),      # 18 x 16 = 288 tiles
     ("256x128 relu", [1000, 3000, 2000, 500], "relu", 2600),             # 11 x 24 tiles
-    ("128x128 sigmoid ragged n", [700, 1001, 515, 300], "sigmoid", 1500),
-    ("n % 4 != 0 leaky", [333, 257, 259, 17], "leaky", 777),
+    ("128x128 sigmoid ragged n", [700, 2004, 1516, 300], "sigmoid", 1500),  # 1516 -> 300 splits K
+    ("ragged n leaky", [333, 260, 259, 20], "leaky", 777),  # 259 % 4 != 0: not fused
     ("four fused tanh", [256, 384, 512, 384, 130], "tanh", 300),
 ]
 
@@ -73,10 +103,12 @@ def test_fused_requant_without_capture(rg, ref, name, dims, act, rows):
     x = rg.randn([rows, dims[0]])
     prof = _run_plain(rg, ref, layers, x, name)
     gemm_ops = [r for r in prof.records if "Gemm" in r.op]
-    # every Linear after the first reads an operand its producer quantized:
-    # no launch precedes its GEMM inside the op
-    for r in gemm_ops[1:]:
-        assert r.duration_ns == r.kernel_ns, r
+    fused = _expected_fused(dims, rows)
+    assert any(fused), "the case must exercise the fused path"
+    # a Linear whose operand its producer quantized launches nothing before
+    # its GEMM; the others run their absmax / quantize kernels first
+    for r, f in zip(gemm_ops[1:], fused):
+        assert (r.duration_ns == r.kernel_ns) == f, (r, f)
 
 
 @pytest.mark.parametrize("name,dims,act,rows", CASES[:3] + CASES[4:], ids=[c[0] for c in CASES[:3] + CASES[4:]])
@@ -106,5 +138,6 @@ def test_linear_stack_full_without_capture(rg, ref):
     model, x = configs.linear_stack()
     layers = model.export()
     prof = _run_plain(rg, ref, layers, x, "stack 4096 gelu full (no capture)")
+    assert _expected_fused([4096] * 5, 8192) == [True] * 3
     for r in prof.records[1:]:
         assert r.duration_ns == r.kernel_ns, r
