@@ -429,6 +429,24 @@ RG_HD int8_t quantize_one(float v, float inv) {
   return (int8_t)(int)t;
 }
 
+// quantize_one's integer for t = v * inv in fewer operations (the fused
+// requantization's form): s = t + copysign(0.5 - 2^-25, t), rounded to f32,
+// then truncated toward zero, is round-half-away(t) for every t.  The
+// addition is exact or rounds to the correct side of each integer boundary;
+// checked on all 2^32 inputs on the host (tests/support/quant_host_check.cpp).
+// The conversion saturates and maps NaN to 0 (the device's v_cvt_i32_f32;
+// restated on the host), and the clamp to +-127 is done on the integer.
+RG_HD int32_t quantize_rz(float t) {
+  const float s = t + __builtin_copysignf(bitsf(0x3effffffu), t);
+#if defined(__HIP_DEVICE_COMPILE__)
+  int32_t i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(s));
+#else
+  const int32_t i = s != s ? 0 : (s >= 2147483648.0f ? 2147483647 : (s <= -2147483648.0f ? (-2147483647 - 1) : (int32_t)s));
+#endif
+  return i < -127 ? -127 : (i > 127 ? 127 : i);
+}
+
 // round_fp16 (quantize.rs:50-64): half an ulp added to the magnitude, then
 // the low 13 mantissa bits cleared (ties away from zero); exponents below
 // -14 give +0 and above 15 give +-65504 (NaN and inf included).  The

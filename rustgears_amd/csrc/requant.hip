@@ -72,20 +72,8 @@ __device__ __forceinline__ LaneSpan lane_span(int32_t wrow0, int32_t wcol0, int3
   return s;
 }
 
-// quantize_one (quantize.rs:22) without branches: v * inv rounded half away
-// from zero (trunc, then +-1 when the dropped fraction is at least 0.5; the
-// fraction x - trunc(x) is exact), converted by the hardware's saturating
-// v_cvt_i32_f32 (NaN -> 0, +-inf and out-of-range values -> +-(2^31 - 1)),
-// then clamped to +-127 as an integer.  The rounded value is an integer, so
-// clamping before or after the conversion agrees: the result equals
-// round, clamp(-127, 127), `as i8` for every input, NaN and infinities
-// included.
-__device__ __forceinline__ int32_t q8(float v, float inv) {
-  const float r = __builtin_roundf(v * inv);
-  int32_t i;
-  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(r));
-  return i < -127 ? -127 : (i > 127 ? 127 : i);
-}
+// quantize_one (quantize.rs:22) without branches (rgmath::quantize_rz).
+__device__ __forceinline__ int32_t q8(float v, float inv) { return rgmath::quantize_rz(v * inv); }
 
 // Four quantized bytes of one row, little-endian by column.
 __device__ __forceinline__ uint32_t q8x4(v4f v, float inv) {

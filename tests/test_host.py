@@ -192,6 +192,20 @@ def test_devmath_matches_host_libm_sampled(tmp_path):
         assert int(bad) == 0, f"{name}: {bad} mismatches vs libm, first input 0x{first}"
 
 
+def test_fast_quantizer_matches_quantize_rule(tmp_path):
+    """rgmath::quantize_rz, the fused requantization's quantizer (one add,
+    a truncating saturating conversion and an integer clamp), against the rule
+    of quantize.rs:22 (round half away from zero, clamp +-127, NaN -> 0) on
+    every 13th f32 bit pattern; all 2^32 with RG_EXHAUSTIVE=1."""
+    exe = tmp_path / "qcheck"
+    src = os.path.join(ROOT, "tests", "support", "quant_host_check.cpp")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-pthread", "-o", str(exe), src], check=True)
+    stride = "1" if os.environ.get("RG_EXHAUSTIVE") == "1" else "13"
+    out = subprocess.run([str(exe), stride, "0", str(min(8, os.cpu_count() or 1))], check=True, capture_output=True,
+                         text=True).stdout.split()
+    assert int(out[0]) >= (1 << 32) // 13 and int(out[1]) == 0, f"first mismatch at 0x{out[2]}"
+
+
 def test_program_create_fails_loudly_without_gpu(rg):
     if rg.device_count() > 0:
         pytest.skip("a GPU is present")
