@@ -135,6 +135,27 @@ int rgnpu_program_run_device(rgnpu_program* prog, const float* d_x, const int64_
                              float* d_y, int64_t y_cap, int64_t* y_shape, int32_t* y_ndim);
 int rgnpu_program_synchronize(rgnpu_program* prog);
 
+/* Allocation-free variant of rgnpu_program_run_device, with the same
+ * arguments and results.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc).  The call makes no hipMalloc or
+ * hipFree: every intermediate buffer of the run (activations between ops,
+ * the i8 / binary16 GEMM operands, absmax slots, scales, conv coverage
+ * masks, split-K partial sums) is a view into one device array of
+ * RGNPU_NOALLOC_SCRATCH_BYTES per GPU, which the library looks up when a
+ * program is created on that GPU and keeps until the process ends.  A shape
+ * whose buffers do not fit gives RGNPU_ERR_CAPACITY (nothing is enqueued);
+ * capture mode gives RGNPU_ERR_INVALID.  Every call on a GPU shares that GPU's
+ * array and finds the previous call's contents (each call clears what must
+ * start at zero), so calls whose device work overlaps on one GPU race:
+ * calls on one program are ordered by its stream, calls on different
+ * programs must be ordered by the caller.  The call records no profile
+ * (last_npu_profile is unchanged).  Host-side bookkeeping for a new input
+ * shape (the plan) uses the host heap. */
+#define RGNPU_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int rgnpu_program_run_device_noalloc(rgnpu_program* prog, const float* d_x, const int64_t* shape, int32_t ndim,
+                                     float* d_y, int64_t y_cap, int64_t* y_shape, int32_t* y_ndim);
+
 /* Throughput measurement on device buffers: enqueues `iters` runs back to
  * back on the program's stream, bracketed by two HIP events, waits, and
  * returns the elapsed device time.  `flags`:

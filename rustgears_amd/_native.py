@@ -75,6 +75,8 @@ SIGNATURES = [
     ("rgnpu_program_run_device", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, i64p, ctypes.c_int32,
                                                 ctypes.c_void_p, ctypes.c_int64, i64p, i32p]),
     ("rgnpu_program_synchronize", ctypes.c_int, [ctypes.c_void_p]),
+    ("rgnpu_program_run_device_noalloc", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, i64p, ctypes.c_int32,
+                                                        ctypes.c_void_p, ctypes.c_int64, i64p, i32p]),
     ("rgnpu_program_benchmark", ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, i64p, ctypes.c_int32,
                                                ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                                                ctypes.POINTER(ctypes.c_double), ctypes.c_void_p, ctypes.c_int32]),

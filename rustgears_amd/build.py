@@ -31,7 +31,7 @@ COMMON = [
     "-I", os.path.join(HERE, "..", "include"),
 ]
 
-SOURCES = ["kernels.hip", "requant.hip", "program.cpp", "hostcopy.cpp", "rng.cpp", "rtim.cpp"]
+SOURCES = ["kernels.hip", "requant.hip", "scratch.hip", "program.cpp", "hostcopy.cpp", "rng.cpp", "rtim.cpp"]
 
 
 def _compile(src: str) -> str:

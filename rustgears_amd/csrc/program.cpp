@@ -49,17 +49,26 @@ struct Error : std::runtime_error {
 struct DevBuf {
   void* p = nullptr;
   size_t bytes = 0;
+  bool borrowed = false;  // a view into memory the buffer does not own (the device scratch)
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
   ~DevBuf() { release(); }
   void release() {
-    if (p) (void)hipFree(p);
+    if (p && !borrowed) (void)hipFree(p);
     p = nullptr;
     bytes = 0;
+    borrowed = false;
+  }
+  void borrow(void* base, size_t n) {
+    release();
+    p = base;
+    bytes = n;
+    borrowed = true;
   }
   void ensure(size_t n) {
     if (n <= bytes && p) return;
+    if (borrowed) throw Error(RGNPU_ERR_INVALID, "internal: growing a view into the device scratch");
     release();
     size_t b = n ? n : 16;
     RG_HIP(hipMalloc(&p, b));
@@ -155,6 +164,11 @@ struct Plan {
   DevBuf ylo;  // FP16 conv: GEMM output [n*L, O] before the NCHW transpose
   DevBuf ws;  // split-K partial sums
   int64_t ws_bytes = 0;
+  // Allocation-free plan: every buffer above is a view into the device
+  // scratch, which other calls overwrite, so each run zeroes its slots and
+  // uploads the coverage masks again (kept here).
+  bool in_scratch = false;
+  std::vector<uint8_t> mask_host;
   std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
   bool capture_ready = false;
   // Per op, indices into the run's launch events (-1 = the run-start event):
@@ -175,6 +189,8 @@ struct rgnpu_program {
   int64_t fp32_bytes = 0, npu_bytes = 0;
   std::vector<std::shared_ptr<Op>> ops;  // device weights; shared with the workers
   std::unique_ptr<Plan> plan;
+  std::unique_ptr<Plan> scratch_plan;  // plan of rgnpu_program_run_device_noalloc
+  void* scratch = nullptr;             // this device's scratch array (scratch.hip)
   int profiling = 1;
   bool capture = false;
   bool capture_valid = false;
@@ -598,7 +614,9 @@ static int64_t numel(const std::vector<int64_t>& s) {
   return n;
 }
 
-static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
+// With `scratch` the plan's buffers are views into that device array (of
+// kScratchBytes) instead of allocations of their own.
+static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, int ndim, void* scratch = nullptr) {
   if (ndim < 1 || ndim > 8) throw Error(RGNPU_ERR_SHAPE, "input rank must be 1..8");
   auto plan = std::make_unique<Plan>();
   plan->in_shape.assign(shape, shape + ndim);
@@ -784,6 +802,41 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
         slots > 0 && (op.kind == OP_LINEAR || op.kind == OP_CONV) && pl.explicit_absmax && pl.in_len > 0;
     break;
   }
+  if (scratch) {
+    // One call's buffers, 256-byte aligned, one after the other.  A new
+    // call finds whatever the previous one (of any program on this device)
+    // left, so the slots are zeroed by every run rather than by the first
+    // kernel of the run before.
+    plan->clear_by_first = false;
+    plan->slot_set_words = round_up(std::max<int64_t>(slots, 1), kSpreadStride);
+    DevBuf* const bufs[] = {&plan->f32[0], &plan->f32[1], &plan->q,     &plan->q_alt, &plan->ylo,
+                            &plan->ws,     &plan->slots,  &plan->scales, &plan->masks};
+    const size_t sizes[] = {plan->f32_elems * sizeof(float),
+                            plan->f32_elems * sizeof(float),
+                            plan->q_bytes,
+                            any_requant ? plan->q_bytes : 0,
+                            plan->ylo_elems * sizeof(float),
+                            (size_t)plan->ws_bytes,
+                            (size_t)plan->slot_set_words * sizeof(uint32_t),
+                            (size_t)std::max<int64_t>(n_scales, 1) * sizeof(float),
+                            mask_host.size()};
+    size_t need = 0;
+    for (size_t b : sizes) need += round_up((int64_t)std::max<size_t>(b, 1), 256);
+    if (need > (size_t)kScratchBytes)
+      throw Error(RGNPU_ERR_CAPACITY, "this input shape needs " + std::to_string(need) +
+                                          " bytes of intermediate buffers; the allocation-free entry point's "
+                                          "device scratch holds " + std::to_string(kScratchBytes) +
+                                          " (use rgnpu_program_run_device)");
+    size_t off = 0;
+    for (size_t k = 0; k < sizeof sizes / sizeof sizes[0]; k++) {
+      const size_t b = std::max<size_t>(sizes[k], 1);
+      bufs[k]->borrow(static_cast<char*>(scratch) + off, b);
+      off += round_up((int64_t)b, 256);
+    }
+    plan->in_scratch = true;
+    plan->mask_host = std::move(mask_host);
+    return plan;
+  }
 
   plan->f32[0].ensure(plan->f32_elems * sizeof(float));
   plan->f32[1].ensure(plan->f32_elems * sizeof(float));
@@ -897,6 +950,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
   if (cap) ensure_capture_buffers(P, plan);
   plan.roles.assign(P->ops.size(), std::array<int, 3>{-1, -1, -1});
   if (ev) RG_HIP(hipEventRecord(ev[0], s));
+  if (plan.in_scratch && !plan.mask_host.empty())
+    RG_HIP(hipMemcpyAsync(plan.masks.p, plan.mask_host.data(), plan.mask_host.size(), hipMemcpyHostToDevice, s));
   uint32_t* const slot_sets = plan.slots.as<uint32_t>();
   uint32_t* slots = slot_sets;
   SlotClear clear{};  // handed to the run's first kernel, then reset
@@ -1222,6 +1277,8 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
     load_code_object(P->stream);
     RG_HIP(hipGetLastError());
     RG_HIP(hipStreamSynchronize(P->stream));
+    // this device's copy of the allocation-free entry point's scratch
+    RG_HIP(scratch_address(device, &P->scratch));
     compile(P.get(), layers, n_layers);
   } catch (...) {
     (void)hipStreamDestroy(P->stream);
@@ -1365,6 +1422,33 @@ int rgnpu_program_run_device(rgnpu_program* P, const float* d_x, const int64_t* 
   if (!d_x && plan.in_len > 0) throw Error(RGNPU_ERR_INVALID, "x is NULL");
   if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
   enqueue_profiled(P, plan, d_x, d_y);
+  RG_API_END
+}
+
+static_assert(kScratchBytes == RGNPU_NOALLOC_SCRATCH_BYTES, "the header states the scratch size");
+
+int rgnpu_program_run_device_noalloc(rgnpu_program* P, const float* d_x, const int64_t* shape, int32_t ndim,
+                                     float* d_y, int64_t y_cap, int64_t* y_shape, int32_t* y_ndim) {
+  RG_API_BEGIN
+  if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(P->mu);
+  if (P->capture)
+    throw Error(RGNPU_ERR_INVALID, "capture mode allocates its tap buffers: use rgnpu_program_run_device");
+  if (!P->scratch) throw Error(RGNPU_ERR_DEVICE, "no device scratch for this program");
+  RG_HIP(hipSetDevice(P->device));
+  Plan* plan = P->scratch_plan.get();
+  if (!plan || (int)plan->in_shape.size() != ndim || !std::equal(plan->in_shape.begin(), plan->in_shape.end(), shape)) {
+    // the previous plan's mask upload may still read its host copy
+    if (plan) RG_HIP(hipStreamSynchronize(P->stream));
+    P->scratch_plan.reset();
+    P->scratch_plan = make_plan(P, shape, ndim, P->scratch);
+    plan = P->scratch_plan.get();
+  }
+  write_shape(*plan, y_shape, y_ndim);
+  if (!d_y) return RGNPU_OK;
+  if (!d_x && plan->in_len > 0) throw Error(RGNPU_ERR_INVALID, "x is NULL");
+  if (y_cap < plan->out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
+  enqueue(P, *plan, d_x, d_y, nullptr, false);
   RG_API_END
 }
 

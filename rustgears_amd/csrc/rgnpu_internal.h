@@ -79,6 +79,13 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 // code object: kernels.hip and requant.hip).
 void load_code_object(hipStream_t s);
 void load_requant_code_object(hipStream_t s);
+
+// Device scratch of the allocation-free run entry point (scratch.hip): one
+// file-scope array of kScratchBytes per device.  scratch_address looks up
+// this device's copy (the device must be current) on its first call for the
+// device and returns the cached address afterwards.
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+hipError_t scratch_address(int device, void** out);
 // Reads `bytes` (a zero-filled buffer) to displace the memory-side cache.
 void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s);
 
