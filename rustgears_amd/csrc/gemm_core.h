@@ -42,6 +42,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// Zeroes the other run's slot set (the plan's slots are double-buffered by
+// run parity and the first kernel of a run clears the set the next run
+// uses).  Every thread of the grid takes a share.
+__device__ __forceinline__ void clear_slots(const SlotClear& c) {
+  if (!c.p) return;
+  const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * blockDim.x;
+  for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < c.n; i += nthreads)
+    c.p[i] = 0u;
+}
+
 __device__ __forceinline__ float slot_scale(const uint32_t* slot) {
   return rgmath::scale_from_absmax(rgmath::bitsf(*slot));
 }

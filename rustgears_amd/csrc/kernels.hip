@@ -104,16 +104,6 @@ __device__ __forceinline__ void block_max_atomic(uint32_t m, uint32_t* slot, boo
   }
 }
 
-// Zeroes the other run's slot set (the plan's slots are double-buffered by
-// run parity and the first kernel of a run clears the set the next run
-// uses).  Every thread of the grid takes a share.
-__device__ __forceinline__ void clear_slots(const SlotClear& c) {
-  if (!c.p) return;
-  const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * blockDim.x;
-  for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x; i < c.n; i += nthreads)
-    c.p[i] = 0u;
-}
-
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int64_t per_img,
                                                      uint32_t* __restrict__ slots, int spread, SlotClear clear) {
   clear_slots(clear);

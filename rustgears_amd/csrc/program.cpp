@@ -143,6 +143,10 @@ struct OpPlan {
   int64_t sync_base = -1;     // its barrier words in the slot set
   bool q_ready = false;       // this op's i8 operand was written by its producer
   int q_in = 0;               // which of the two i8 operand buffers this op's GEMM reads
+  // INT8 Linear quantizing its own input (explicit absmax): the one-pass
+  // kernel's barrier words in the slot set, or -1 for the absmax + quantize
+  // kernel pair.
+  int64_t iq_sync_base = -1;
 };
 
 struct Plan {
@@ -789,6 +793,17 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     cpl.q_in = pl.q_in ^ 1;
     any_requant = true;
   }
+  // A Linear that quantizes its own input does so in one pass when the
+  // shapes fit the kernel's 32-bit offsets.
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
+    const Op& op = *P->ops[i];
+    OpPlan& pl = plan->ops[i];
+    if (op.kind != OP_LINEAR || !pl.explicit_absmax || pl.rows <= 0 ||
+        !input_quant_supported(pl.rows, op.in_f, pl.Mpad, op.Kpad))
+      continue;
+    pl.iq_sync_base = round_up(slots, kSpreadStride);
+    slots = pl.iq_sync_base + input_quant_sync_words(pl.Mpad, op.Kpad);
+  }
   if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
   else plan->spin_limit = 100000;  // ~20 ms
   plan->n_slots = slots;
@@ -1036,7 +1051,11 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         }
         uint32_t* slot = slots + pl.slot_base;
         int8_t* const qa = pl.q_in ? plan.q_alt.as<int8_t>() : q;
-        if (!pl.q_ready) {
+        if (pl.iq_sync_base >= 0) {
+          launch_input_quant(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base,
+                             slots + pl.iq_sync_base, plan.spin_limit, clear, s);
+          first_launched();
+        } else if (!pl.q_ready) {
           if (pl.explicit_absmax) {
             launch_absmax(in, pl.in_len, 1, slot, true, nullptr, nullptr, 0, 0, s, clear);
             first_launched();

@@ -53,6 +53,64 @@ constexpr int kFinisherExtraPolls = 100000;     // settle budget of the finisher
 static_assert(kError < kRequantStateBase, "state words follow the counters");
 }  // namespace rqk
 
+// Arrival at the grid barrier of a persistent launch; every thread of the
+// workgroup calls it after the workgroup's absmax atomic has completed.
+// Two-level arrival: the last of a group counts the group, and the arrival
+// that completes the last group is the finisher, which releases every other
+// workgroup through its go line.  Returns 2 for the finisher, 1 for a
+// released workgroup, 0 for one that gave up after spin_limit polls.
+// blk_flag is a word of the workgroup's LDS.
+__device__ __forceinline__ uint32_t grid_arrive(uint32_t* sync, int b, int G, int spin_limit, uint32_t* blk_flag) {
+  if (threadIdx.x == 0) {
+    const int g = b % rqk::kGroups;
+    const uint32_t in_group = (uint32_t)((G - g + rqk::kGroups - 1) / rqk::kGroups);
+    const uint32_t groups = (uint32_t)(G < rqk::kGroups ? G : rqk::kGroups);
+    uint32_t flag = 0;
+    if (__hip_atomic_fetch_add(sync + g * rqk::kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            in_group &&
+        __hip_atomic_fetch_add(sync + rqk::kGroupDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups)
+      flag = 2;
+    uint32_t* const go = sync + rqk::kGoBase + (int64_t)b * rqk::kLine;
+    for (int k = 0; flag == 0 && k < spin_limit; k++) {
+      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
+      if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) flag = 1;
+    }
+    *blk_flag = flag;
+  }
+  __syncthreads();
+  const uint32_t flag = *blk_flag;
+  if (flag == 2) {
+    // release every other workgroup: one line each
+    for (int w = threadIdx.x; w < G; w += blockDim.x)
+      if (w != b)
+        __hip_atomic_store(sync + rqk::kGoBase + (int64_t)w * rqk::kLine, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return flag;
+}
+
+// The finisher's wait for every workgroup's state word (each is running, so
+// this is short; one that never settles raises the error flag): the indices
+// of the deferred ones go to list[0 .. *count).  Every thread calls it;
+// count is a word of LDS.
+__device__ __forceinline__ int collect_deferred(uint32_t* sync, int G, int spin_limit, uint32_t* list,
+                                                uint32_t* count) {
+  if (threadIdx.x == 0) *count = 0;
+  __syncthreads();
+  for (int w = threadIdx.x; w < G; w += blockDim.x) {
+    uint32_t st = 0;
+    for (int k = 0; k < spin_limit + rqk::kFinisherExtraPolls; k++) {
+      st = __hip_atomic_load(sync + kRequantStateBase + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (st != 0) break;
+      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
+    }
+    if (st == 0) __hip_atomic_store(sync + rqk::kError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (st == rqk::kDeferred) list[atomicAdd(count, 1u)] = (uint32_t)w;
+  }
+  __syncthreads();
+  return (int)*count;
+}
+
 // The lane layout of the requant epilogue and quantization: lane l of a
 // wave owning rows [wrow0, wrow0 + 16 FM) and columns [wcol0, wcol0 + 64)
 // takes the 4 consecutive columns wcol0 + 4 (l & 15) .. + 3 of rows
@@ -300,34 +358,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
     }
   }
   __builtin_amdgcn_s_barrier();
-  if (tid == 0) {
-    // two-level arrival: the last of a group counts the group, the arrival
-    // that completes the last group is the finisher
-    const int g = b % rqk::kGroups;
-    const uint32_t in_group = (uint32_t)((G - g + rqk::kGroups - 1) / rqk::kGroups);
-    const uint32_t groups = (uint32_t)(G < rqk::kGroups ? G : rqk::kGroups);
-    uint32_t flag = 0;
-    if (__hip_atomic_fetch_add(rq.sync + g * rqk::kLine, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-            in_group &&
-        __hip_atomic_fetch_add(rq.sync + rqk::kGroupDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-            groups)
-      flag = 2;
-    uint32_t* const go = rq.sync + rqk::kGoBase + (int64_t)b * rqk::kLine;
-    for (int k = 0; flag == 0 && k < rq.spin_limit; k++) {
-      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
-      if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) flag = 1;
-    }
-    blk[0] = flag;
-  }
-  __syncthreads();
-  const uint32_t flag = blk[0];
-  if (flag == 2) {
-    // release every other workgroup: one line each
-    for (int w = tid; w < G; w += blockDim.x)
-      if (w != b)
-        __hip_atomic_store(rq.sync + rqk::kGoBase + (int64_t)w * rqk::kLine, 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-  }
+  const uint32_t flag = grid_arrive(rq.sync, b, G, rq.spin_limit, &blk[0]);
   const LaneSpan sp_last = lane_span(m0 + wrow, n0 + wcolw, M, N, lane);
   if (flag == 0) {
     // Waited too long: the finisher quantizes this workgroup's tiles from the
@@ -360,20 +391,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
   // Finisher: the scale tap, then the tiles of every deferred workgroup.
   if (tid == 0 && rq.scale_out) *rq.scale_out = scale;
   uint32_t* list = reinterpret_cast<uint32_t*>(smem);  // the ring is free: no K loop follows
-  if (tid == 0) blk[1] = 0;
-  __syncthreads();
-  for (int w = tid; w < G; w += blockDim.x) {
-    uint32_t st = 0;
-    for (int k = 0; k < rq.spin_limit + rqk::kFinisherExtraPolls; k++) {
-      st = __hip_atomic_load(rq.sync + kRequantStateBase + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (st != 0) break;
-      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
-    }
-    if (st == 0) __hip_atomic_store(rq.sync + rqk::kError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (st == rqk::kDeferred) list[atomicAdd(&blk[1], 1u)] = (uint32_t)w;
-  }
-  __syncthreads();
-  const int ndef = (int)blk[1];
+  const int ndef = collect_deferred(rq.sync, G, rq.spin_limit, list, &blk[1]);
   if (ndef > 0) __threadfence();  // acquire: the deferred workgroups' stored outputs
   for (int d = 0; d < ndef; d++) {
     const int w = (int)list[d];
@@ -418,6 +436,279 @@ static void launch_requant_shape(const int8_t* A, const int8_t* B, const Requant
     default: RG_RQ(rgmath::ACT_NONE); break;
   }
 #undef RG_RQ
+}
+
+// ---------------------------------------------------------------------------
+// A Linear's input quantization in one pass: QuantTensor::from_f32
+// (quantize.rs:18-24) at npu.rs:312 for an input that no fused producer has
+// quantized (the run's input, or the output of an op that does not emit the
+// absmax).  The operand q [Mpad, Kpad] is cut into 4-byte units (4 inputs of
+// one row; padding rows and columns are zero) and thread t of a grid of NT
+// threads owns units t, t + NT, ..., so one load of a wave reads 1 KiB of
+// consecutive inputs and one store writes 256 consecutive bytes.  A
+// persistent grid reads its units once and keeps U of them per thread (the
+// smallest U of 4, 8, ..., 64 whose grid is resident; at U = 64 the first 19
+// in LDS and 45 in registers, 1 KiB of input per thread: the whole 134 MB
+// input of an 8192 x 4096 batch on 256 CUs), raises the spread absmax slot,
+// meets at the grid barrier and quantizes what it kept; units beyond those
+// (inputs larger than the resident grid keeps) are read a second time.  The separate absmax pass
+// over the input, and its launch, are gone.  A workgroup that waits too long
+// at the barrier just exits: the finisher quantizes its units from the
+// input, which nothing has changed.  A grid of one workgroup needs no
+// barrier.
+// ---------------------------------------------------------------------------
+namespace iq {
+constexpr int kThreads = 512;
+constexpr int kMaxRegUnits = 45;  // units per thread in registers at most (180 VGPRs)
+constexpr int kFirst = 30;        // register units loaded together with the LDS units
+// units kept per thread: U, of which lds_units(U) in LDS (152 KiB per workgroup at U = 64)
+constexpr int lds_units(int U) { return U > kMaxRegUnits ? U - kMaxRegUnits : 0; }
+}  // namespace iq
+
+struct InputQuantShape {
+  int32_t M, K;     // input rows and row length (floats)
+  uint32_t upr;     // units per operand row (Kpad / 4)
+  uint32_t W;       // units of the operand (Mpad * Kpad / 4)
+  uint32_t dr, dc;  // NT = dr * upr + dc: the row and unit-column step between a thread's units
+};
+
+// Next unit of this thread: w += NT in (row, unit-column) form.
+__device__ __forceinline__ void iq_step(uint32_t& r, uint32_t& c, const InputQuantShape& s) {
+  c += s.dc;
+  r += s.dr;
+  const bool carry = c >= s.upr;
+  c = carry ? c - s.upr : c;
+  r = carry ? r + 1 : r;
+}
+
+// The 4 inputs of unit (r, c): zeros outside [M, K] (loads out of the input
+// are dropped, and a dropped buffer load returns 0).
+template <bool VEC>
+__device__ __forceinline__ v4f iq_load(__amdgpu_buffer_rsrc_t rx, uint32_t r, uint32_t c, const InputQuantShape& s) {
+  const uint32_t c0 = c * 4u;
+  const bool row_ok = r < (uint32_t)s.M;
+  const uint32_t base = (r * (uint32_t)s.K + c0) * 4u;  // used only in bounds (input < 2^31 bytes)
+  if constexpr (VEC) {
+    const bool ok = row_ok && c0 < (uint32_t)s.K;  // K % 4 == 0: a unit is all in or all out
+    return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? base : kDropOffset), 0, 0));
+  } else {
+    v4f v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const bool ok = row_ok && c0 + e < (uint32_t)s.K;
+      v[e] = __builtin_bit_cast(float,
+                                __builtin_amdgcn_raw_buffer_load_b32(rx, (int)(ok ? base + 4u * e : kDropOffset), 0, 0));
+    }
+    return v;
+  }
+}
+
+__device__ __forceinline__ float iq_absmax(float m, v4f v) {
+  m = __builtin_fmaxf(m, __builtin_fabsf(v[0]));  // NaN ignored, like f32::max
+  m = __builtin_fmaxf(m, __builtin_fabsf(v[1]));
+  m = __builtin_fmaxf(m, __builtin_fabsf(v[2]));
+  return __builtin_fmaxf(m, __builtin_fabsf(v[3]));
+}
+
+// Unit w of the operand (byte offset 4 w); units past the operand are dropped.
+__device__ __forceinline__ void iq_store(__amdgpu_buffer_rsrc_t rq, v4f v, float inv, uint32_t w, uint32_t W) {
+  __builtin_amdgcn_raw_buffer_store_b32(q8x4(v, inv), rq, (int)(w < W ? w * 4u : kDropOffset), 0, 0);
+}
+
+// Quantizes the units w, w + NT, ... of one thread from the input (units
+// beyond the kept ones, and the finisher's share of a deferred workgroup).
+template <bool VEC>
+__device__ __forceinline__ void iq_quantize_from(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rq,
+                                                 const InputQuantShape& s, uint32_t w, uint32_t NT, uint32_t r,
+                                                 uint32_t c, float inv) {
+  for (; w < s.W; w += NT) {
+    iq_store(rq, iq_load<VEC>(rx, r, c, s), inv, w, s.W);
+    iq_step(r, c, s);
+  }
+}
+
+template <bool VEC, int U>
+__global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* __restrict__ x, InputQuantShape sh,
+                                                                   uint32_t* __restrict__ slot, int8_t* q,
+                                                                   float* scale_out, uint32_t* sync, int spin_limit,
+                                                                   SlotClear clear) {
+  using namespace iq;
+  constexpr int KL = lds_units(U), KR = U - KL;
+  static_assert(KR <= kMaxRegUnits && (KL == 0 || KR >= kFirst), "unit split");
+  // one LDS array: the LDS units as [KL][kThreads] 16-byte words, 16 words
+  // of block state, then the finisher's list of deferred workgroups
+  constexpr int kListWords = (int)rqk::kMaxGrid;
+  __shared__ __attribute__((aligned(16))) v4f lds[KL * kThreads + 4 + kListWords / 4];
+  uint32_t* const blk = reinterpret_cast<uint32_t*>(lds + KL * kThreads);  // [0] flag, [1] count, [2..] wave maxima
+  clear_slots(clear);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = (int)gridDim.x, b = (int)blockIdx.x;
+  const uint32_t NT = (uint32_t)G * kThreads, gtid = (uint32_t)b * kThreads + (uint32_t)tid;
+  const __amdgpu_buffer_rsrc_t rx = bounded_rsrc(x), rq = bounded_rsrc(q);
+  const uint32_t r0 = gtid / sh.upr, c0 = gtid - r0 * sh.upr;
+
+  // Pass 1: read every unit once (units past the operand have r >= Mpad >=
+  // M and read as zeros).  Units 0 .. KL-1 of the thread go to LDS, the next
+  // KR stay in registers, later ones are only measured.  The LDS units'
+  // loads and the first kFirst register units' are in flight together; the
+  // LDS units are retired before the other register units are loaded, so at
+  // most KR units occupy registers at a time.
+  v4f keep[KR];
+  float m = 0.0f;
+  uint32_t r = r0, c = c0;
+  if constexpr (KL > 0) {
+    v4f part[KL];
+#pragma unroll
+    for (int j = 0; j < KL; j++) {
+      part[j] = iq_load<VEC>(rx, r, c, sh);
+      iq_step(r, c, sh);
+    }
+#pragma unroll
+    for (int j = 0; j < kFirst; j++) {
+      keep[j] = iq_load<VEC>(rx, r, c, sh);
+      iq_step(r, c, sh);
+    }
+#pragma unroll
+    for (int j = 0; j < KL; j++) {
+      m = iq_absmax(m, part[j]);
+      lds[j * kThreads + tid] = part[j];
+    }
+  }
+#pragma unroll
+  for (int j = KL > 0 ? kFirst : 0; j < KR; j++) {
+    keep[j] = iq_load<VEC>(rx, r, c, sh);
+    iq_step(r, c, sh);
+  }
+#pragma unroll
+  for (int j = 0; j < KR; j++) m = iq_absmax(m, keep[j]);
+  const uint32_t rest_r = r, rest_c = c;
+  const uint32_t rest_w = gtid + (uint32_t)U * NT;
+  for (uint32_t w = rest_w; w < sh.W; w += NT) {
+    m = iq_absmax(m, iq_load<VEC>(rx, r, c, sh));
+    iq_step(r, c, sh);
+  }
+  // the workgroup's absmax: one atomic into its partial of the spread slot
+  const uint32_t mw = wave_max_u32(rgmath::fbits(m));
+  if (lane == 0) blk[2 + wave] = mw;
+  __syncthreads();
+  uint32_t t = blk[2];
+  for (int w = 1; w < kThreads / 64; w++) t = blk[2 + w] > t ? blk[2 + w] : t;
+  if (tid == 0) {
+    if (t) atomicMax(slot + (b & (kSpread - 1)) * kSpreadStride, t);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the atomic has completed before the arrival
+  }
+  uint32_t flag = 2;  // a grid of one is its own finisher, and its absmax is t
+  float scale;
+  if (G == 1) {
+    scale = rgmath::scale_from_absmax(rgmath::bitsf(t));
+  } else {
+    flag = grid_arrive(sync, b, G, spin_limit, &blk[0]);
+    if (flag == 0) {
+      // waited too long: the finisher quantizes this workgroup's units
+      if (tid == 0)
+        __hip_atomic_store(sync + kRequantStateBase + b, rqk::kDeferred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (tid == 0)
+      __hip_atomic_store(sync + kRequantStateBase + b, rqk::kOwn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t pm = __hip_atomic_load(slot + lane * kSpreadStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    scale = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(pm)));
+  }
+  const float inv = 1.0f / scale;
+  // pass 2: the kept units, then the rest from the input
+#pragma unroll
+  for (int j = 0; j < KL; j++) iq_store(rq, lds[j * kThreads + tid], inv, gtid + (uint32_t)j * NT, sh.W);
+#pragma unroll
+  for (int j = 0; j < KR; j++) iq_store(rq, keep[j], inv, gtid + (uint32_t)(KL + j) * NT, sh.W);
+  iq_quantize_from<VEC>(rx, rq, sh, rest_w, NT, rest_r, rest_c, inv);
+  if (flag != 2) return;
+
+  // Finisher: the scale tap, then the units of every deferred workgroup.
+  if (tid == 0 && scale_out) *scale_out = scale;
+  if (G == 1) return;
+  uint32_t* const list = blk + 16;  // kListWords words after the block state
+  const int ndef = collect_deferred(sync, G, spin_limit, list, &blk[1]);
+  // the thread index again, from the wave index (scalar) and the lane count,
+  // rather than a register held across the whole kernel
+  const uint32_t tid2 = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 64u +
+                        __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  for (int d = 0; d < ndef; d++) {
+    const uint32_t g2 = list[d] * kThreads + tid2;
+    const uint32_t rr = g2 / sh.upr;
+    iq_quantize_from<VEC>(rx, rq, sh, g2, NT, rr, g2 - rr * sh.upr, inv);
+  }
+}
+
+bool input_quant_supported(int64_t M, int64_t K, int64_t Mpad, int64_t Kpad) {
+  // 32-bit byte offsets into the input, the operand, and past them
+  return M > 0 && K > 0 && Kpad % 16 == 0 && M <= Mpad && K <= Kpad && Mpad * Kpad * 4 < ((int64_t)1 << 31);
+}
+
+// The launch: the smallest U (units kept per thread) whose grid of
+// ceil(W / (512 U)) workgroups is resident; else U = 64 on every resident
+// slot (capped by the barrier's kMaxGrid), the rest read twice.
+struct IqLaunch {
+  int U;
+  int64_t G;
+};
+
+template <bool VEC, int U>
+static const void* iq_fn() {
+  return reinterpret_cast<const void*>(&input_quant_kernel<VEC, U>);
+}
+
+template <int U>
+static int64_t iq_cap() {
+  static const int64_t cap = resident_blocks(iq_fn<true, U>(), iq::kThreads);
+  return cap < rqk::kMaxGrid ? cap : rqk::kMaxGrid;
+}
+
+static IqLaunch input_quant_choice(int64_t Mpad, int64_t Kpad) {
+  const int64_t W = Mpad * Kpad / 4;
+  const int64_t caps[5] = {iq_cap<4>(), iq_cap<8>(), iq_cap<16>(), iq_cap<32>(), iq_cap<64>()};
+  for (int i = 0, U = 4; i < 5; i++, U *= 2) {
+    const int64_t per_block = (int64_t)iq::kThreads * U, G = (W + per_block - 1) / per_block;
+    if (G <= caps[i]) return IqLaunch{U, G < 1 ? 1 : G};
+  }
+  return IqLaunch{64, caps[4]};
+}
+
+int64_t input_quant_sync_words(int64_t Mpad, int64_t Kpad) {
+  return rqk::kGoBase + input_quant_choice(Mpad, Kpad).G * rqk::kLine;
+}
+
+template <bool VEC, int U>
+static void launch_iq(const float* x, const InputQuantShape& sh, int64_t G, uint32_t* slot, int8_t* q,
+                      float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+  RG_LAUNCH((input_quant_kernel<VEC, U>), dim3((unsigned)G), dim3(iq::kThreads), 0, s, x, sh, slot, q, scale_out, sync,
+            spin_limit, clear);
+}
+
+template <bool VEC>
+static void launch_iq_u(int U, const float* x, const InputQuantShape& sh, int64_t G, uint32_t* slot, int8_t* q,
+                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+  switch (U) {
+    case 4: launch_iq<VEC, 4>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+    case 8: launch_iq<VEC, 8>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+    case 16: launch_iq<VEC, 16>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+    case 32: launch_iq<VEC, 32>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+    default: launch_iq<VEC, 64>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+  }
+}
+
+void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad, uint32_t* slot, int8_t* q,
+                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+  if (!input_quant_supported(M, K, Mpad, Kpad) || !slot || !q || !sync || (reinterpret_cast<uintptr_t>(q) & 15))
+    throw std::logic_error("input_quant: unsupported shape or missing buffers");
+  const bool vec = K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  const IqLaunch lc = input_quant_choice(Mpad, Kpad);
+  const int64_t W = Mpad * Kpad / 4, NT = lc.G * iq::kThreads, upr = Kpad / 4;
+  const InputQuantShape sh{(int32_t)M, (int32_t)K, (uint32_t)upr, (uint32_t)W, (uint32_t)(NT / upr),
+                           (uint32_t)(NT % upr)};
+  if (vec)
+    launch_iq_u<true>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, clear, s);
+  else
+    launch_iq_u<false>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, clear, s);
 }
 
 // This translation unit is its own code object: loaded at program creation

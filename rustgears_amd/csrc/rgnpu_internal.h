@@ -134,6 +134,17 @@ int64_t requant_sync_words(int64_t Mpad, int64_t Npad, int64_t Kpad);
 void launch_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Mpad, int64_t Npad,
                          int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s);
 
+// A Linear input's quantization in one pass (requant.hip): x f32 [M, K] ->
+// q i8 [Mpad, Kpad] (padding zero) with the per-tensor absmax raised into the
+// spread slot and its scale written to scale_out; a persistent grid that
+// keeps its share of x in registers and LDS across a grid barrier (sync:
+// input_quant_sync_words() zeroed words).  The run's first kernel also
+// zeroes `clear`.  Requires input_quant_supported.
+bool input_quant_supported(int64_t M, int64_t K, int64_t Mpad, int64_t Kpad);
+int64_t input_quant_sync_words(int64_t Mpad, int64_t Kpad);
+void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad, uint32_t* slot, int8_t* q,
+                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s);
+
 // Same contract for M <= 8 rows (weight-streaming GEMV).
 // INT8 Linear with N <= kNarrowMaxN outputs per row: one wave per row, the
 // weights from L1 (A [M,Kpad], B [>= N, Kpad]).

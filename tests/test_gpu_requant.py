@@ -16,7 +16,11 @@ outputs.  These tests check, bit for bit against the oracle:
 * the deferral path: with RGNPU_REQUANT_SPIN_LIMIT=0 no workgroup waits at
   the barrier, and the finisher quantizes every other workgroup's tiles;
 * that a fused consumer launches nothing before its GEMM (its op time equals
-  its kernel time in the profile).
+  its kernel time in the profile);
+* the one-pass quantization of a Linear's own input (a persistent grid that
+  keeps its share of the input in registers and LDS across the barrier): an
+  input larger than what the grid keeps (the rest is read twice), with and
+  without deferral.
 """
 import numpy as np
 import pytest
@@ -141,3 +145,18 @@ def test_linear_stack_full_without_capture(rg, ref):
     assert _expected_fused([4096] * 5, 8192) == [True] * 3
     for r in prof.records[1:]:
         assert r.duration_ns == r.kernel_ns, r
+
+
+@pytest.mark.parametrize("spin", [None, "0"], ids=["resident", "deferred"])
+def test_input_quantization_larger_than_the_grid_keeps(rg, ref, monkeypatch, spin):
+    """8192 x 8192 f32 (256 MiB) into Linear(8192, 40): 32 chunks of 16
+    inputs per thread of a 256-workgroup grid, 16 of them kept; the i8
+    operand and scale taps are compared with the oracle's."""
+    from rustgears_amd import nn
+    if spin is not None:
+        monkeypatch.setenv("RGNPU_REQUANT_SPIN_LIMIT", spin)
+    rg.manual_seed(41)
+    layers = nn.Sequential().add(nn.Linear(8192, 40)).add(nn.Relu()).export()
+    x = rg.randn([8192, 8192])
+    x[5, 7] = -93.25  # the absmax sits in the first kept chunk of one thread
+    check_against_oracle(rg, ref, layers, x, f"input quant 8192x8192 spin={spin}")
