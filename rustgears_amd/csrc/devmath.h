@@ -447,6 +447,22 @@ RG_HD int32_t quantize_rz(float t) {
   return i < -127 ? -127 : (i > 127 ? 127 : i);
 }
 
+// quantize_rz without the clamp, for t = v * inv with |v| at most the absmax
+// the scale was taken from (a tensor quantized with its own absmax): with
+// scale = fl(absmax / 127) and inv = fl(1 / scale), |t| <= 127 (1 + 3 * 2^-24)
+// < 127.5, so the rounded integer is already within +-127 (checked for every
+// finite absmax by tests/support/quant_host_check.cpp).  NaN gives 0.
+RG_HD int32_t quantize_rz_bounded(float t) {
+  const float s = t + __builtin_copysignf(bitsf(0x3effffffu), t);
+#if defined(__HIP_DEVICE_COMPILE__)
+  int32_t i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(s));
+  return i;
+#else
+  return s != s ? 0 : (int32_t)s;
+#endif
+}
+
 // round_fp16 (quantize.rs:50-64): half an ulp added to the magnitude, then
 // the low 13 mantissa bits cleared (ties away from zero); exponents below
 // -14 give +0 and above 15 give +-65504 (NaN and inf included).  The

@@ -130,8 +130,9 @@ __device__ __forceinline__ LaneSpan lane_span(int32_t wrow0, int32_t wcol0, int3
   return s;
 }
 
-// quantize_one (quantize.rs:22) without branches (rgmath::quantize_rz).
-__device__ __forceinline__ int32_t q8(float v, float inv) { return rgmath::quantize_rz(v * inv); }
+// quantize_one (quantize.rs:22) without branches, for a value of the tensor
+// whose absmax gave inv: the clamp to +-127 cannot act (rgmath::quantize_rz_bounded).
+__device__ __forceinline__ int32_t q8(float v, float inv) { return rgmath::quantize_rz_bounded(v * inv); }
 
 // Four quantized bytes of one row, little-endian by column.
 __device__ __forceinline__ uint32_t q8x4(v4f v, float inv) {
@@ -247,38 +248,39 @@ __device__ __forceinline__ void quantize_kept(const v4i (&acc)[FM][4], int8_t* q
     }
 }
 
-// Quantizes one wave's (16 FM) x 64 part of a tile from its stored f32
-// outputs, 4 slabs (16 loads per lane) in flight at a time.  Buffer loads
-// with the row offset in a scalar: no address registers per load.
-template <int FM>
-__device__ __forceinline__ void quantize_stored(const float* y, int8_t* q, int32_t ldq, int32_t wrow0, int32_t wcol0,
-                                                int32_t N, const LaneSpan& sp, float inv, int lane) {
-  constexpr int BATCH = FM < 4 ? FM : 4;
-  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)wrow0 * N + wcol0);
-  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)wrow0 * ldq + wcol0);
-  const uint32_t voff = (uint32_t)(((lane >> 4) * N + 4 * (lane & 15)) * 4);
-  const uint32_t qoff = (uint32_t)((lane >> 4) * ldq + 4 * (lane & 15));
-  const bool q_ok = wcol0 + 4 * (lane & 15) < ldq;
-  const uint32_t row_bytes = (uint32_t)N * 4u;
+// Quantizes a whole BM x BN tile (rows m0.., columns n0..) from its stored
+// f32 outputs, the workgroup's threads walking it row-major: one load of a
+// wave reads 64 consecutive float4 (a 1 KiB row when BN = 256) and one store
+// writes 256 consecutive bytes.  Rows past M and columns past N are the
+// operand's zero padding; columns at or past ldq are not part of it.  BATCH
+// loads per thread are in flight before the first is used.
+template <int BM, int BN, int NTHREADS>
+__device__ __forceinline__ void quantize_stored_flat(const float* y, int8_t* q, int32_t ldq, int32_t m0, int32_t n0,
+                                                     int32_t M, int32_t N, float inv, int tid) {
+  constexpr int C4 = BN / 4, PER = BM * C4 / NTHREADS, BATCH = PER < 16 ? PER : 16;
+  static_assert(PER * NTHREADS == BM * C4 && PER % BATCH == 0 && NTHREADS % C4 == 0, "tile walk");
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)m0 * N + n0);
+  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)m0 * ldq + n0);
+  const int c4 = tid % C4, rt = tid / C4;  // a thread keeps its column; its rows step by NTHREADS / C4
+  constexpr int RSTEP = NTHREADS / C4;
+  const bool col_ok = n0 + 4 * c4 < N, q_ok = n0 + 4 * c4 < ldq;
+  const int32_t rows_left = M - m0 - rt;  // row rt + RSTEP k is an output iff RSTEP k < rows_left
+  const uint32_t voff = (uint32_t)((rt * N + 4 * c4) * 4), qoff = (uint32_t)(rt * ldq + 4 * c4);
 #pragma unroll
-  for (int i0 = 0; i0 < FM; i0 += BATCH) {
-    v4f v[BATCH][4];
+  for (int k0 = 0; k0 < PER; k0 += BATCH) {
+    v4f v[BATCH];
 #pragma unroll
-    for (int i = 0; i < BATCH; i++)
+    for (int k = 0; k < BATCH; k++) {
+      const int rr = (k0 + k) * RSTEP;
+      const bool ok = rr < rows_left && col_ok;
+      v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 0));
+    }
 #pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const int ro = (i0 + i) * 16 + p * 4;
-        const bool ok = ro < sp.rows_left && sp.cols_ok;
-        v[i][p] = __builtin_bit_cast(
-            v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)(ok ? voff : kDropOffset), (int)(ro * row_bytes), 0));
-      }
-#pragma unroll
-    for (int i = 0; i < BATCH; i++)
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const int ro = (i0 + i) * 16 + p * 4;
-        quant_store(rq, v[i][p], inv, qoff, (uint32_t)ro * (uint32_t)ldq, ro < sp.rows_left, sp.cols_ok, q_ok);
-      }
+    for (int k = 0; k < BATCH; k++) {
+      const int rr = (k0 + k) * RSTEP;
+      quant_store(rq, v[k], inv, qoff, (uint32_t)rr * (uint32_t)ldq, rr < rows_left, col_ok, q_ok);
+    }
   }
 }
 
@@ -383,8 +385,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
   for (int it = 0; it + 1 < ntile; it++) {
     int tm, tn;
     tile_coords(b + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
-    const int32_t r0 = tm * BM + wrow, c0 = tn * BN + wcolw;
-    quantize_stored<FM>(ep.y, rq.q, sh.ldq, r0, c0, N, lane_span(r0, c0, M, N, lane), inv, lane);
+    quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
   }
   if (flag != 2) return;
 
@@ -399,8 +400,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
     for (int it = 0; it < wt; it++) {
       int tm, tn;
       tile_coords(w + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
-      const int32_t r0 = tm * BM + wrow, c0 = tn * BN + wcolw;
-      quantize_stored<FM>(ep.y, rq.q, sh.ldq, r0, c0, N, lane_span(r0, c0, M, N, lane), inv, lane);
+      quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
     }
   }
 }
@@ -443,10 +443,14 @@ static void launch_requant_shape(const int8_t* A, const int8_t* B, const Requant
 // (quantize.rs:18-24) at npu.rs:312 for an input that no fused producer has
 // quantized (the run's input, or the output of an op that does not emit the
 // absmax).  The operand q [Mpad, Kpad] is cut into 4-byte units (4 inputs of
-// one row; padding rows and columns are zero) and thread t of a grid of NT
-// threads owns units t, t + NT, ..., so one load of a wave reads 1 KiB of
-// consecutive inputs and one store writes 256 consecutive bytes.  A
-// persistent grid reads its units once and keeps U of them per thread (the
+// one row; padding rows and columns are zero).  Workgroup b of G keeps the
+// U * 512 consecutive units from b * U * 512 on, thread t of it units
+// b U 512 + 512 j + t (j < U), so one load of a wave reads 1 KiB of
+// consecutive inputs, one store writes 256 consecutive bytes, and a
+// workgroup's reads stay within one contiguous range (few pages, long DRAM
+// bursts).  Units past G U 512 (an input larger than the resident grid
+// keeps) are shared out as G U 512 + gtid + k G 512.  A persistent grid
+// reads its units once and keeps U of them per thread (the
 // smallest U of 4, 8, ..., 64 whose grid is resident; at U = 64 the first 19
 // in LDS and 45 in registers, 1 KiB of input per thread: the whole 134 MB
 // input of an 8192 x 4096 batch on 256 CUs), raises the spread absmax slot,
@@ -469,15 +473,16 @@ struct InputQuantShape {
   int32_t M, K;     // input rows and row length (floats)
   uint32_t upr;     // units per operand row (Kpad / 4)
   uint32_t W;       // units of the operand (Mpad * Kpad / 4)
-  uint32_t dr, dc;  // NT = dr * upr + dc: the row and unit-column step between a thread's units
+  uint32_t kr, kc;  // 512 = kr * upr + kc: the (row, unit-column) step between a thread's kept units
+  uint32_t nr, nc;  // NT = G * 512 in the same form: the step between its remaining units
 };
 
-// Next unit of this thread: w += NT in (row, unit-column) form.
-__device__ __forceinline__ void iq_step(uint32_t& r, uint32_t& c, const InputQuantShape& s) {
-  c += s.dc;
-  r += s.dr;
-  const bool carry = c >= s.upr;
-  c = carry ? c - s.upr : c;
+// w += (dr * upr + dc) in (row, unit-column) form.
+__device__ __forceinline__ void iq_step(uint32_t& r, uint32_t& c, uint32_t dr, uint32_t dc, uint32_t upr) {
+  c += dc;
+  r += dr;
+  const bool carry = c >= upr;
+  c = carry ? c - upr : c;
   r = carry ? r + 1 : r;
 }
 
@@ -510,21 +515,32 @@ __device__ __forceinline__ float iq_absmax(float m, v4f v) {
   return __builtin_fmaxf(m, __builtin_fabsf(v[3]));
 }
 
-// Unit w of the operand (byte offset 4 w); units past the operand are dropped.
-__device__ __forceinline__ void iq_store(__amdgpu_buffer_rsrc_t rq, v4f v, float inv, uint32_t w, uint32_t W) {
-  __builtin_amdgcn_raw_buffer_store_b32(q8x4(v, inv), rq, (int)(w < W ? w * 4u : kDropOffset), 0, 0);
+// Unit w of the operand (byte offset 4 w) through a resource whose record
+// count is the operand's size: the hardware drops units past the operand.
+__device__ __forceinline__ void iq_store(__amdgpu_buffer_rsrc_t rq, v4f v, float inv, uint32_t w) {
+  __builtin_amdgcn_raw_buffer_store_b32(q8x4(v, inv), rq, (int)(w * 4u), 0, 0);
 }
 
-// Quantizes the units w, w + NT, ... of one thread from the input (units
-// beyond the kept ones, and the finisher's share of a deferred workgroup).
+// Quantizes `count` units w, w + (dr upr + dc), ... of one thread from the
+// input (starting at row r, unit-column c); units past the operand are
+// dropped.
 template <bool VEC>
 __device__ __forceinline__ void iq_quantize_from(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rq,
-                                                 const InputQuantShape& s, uint32_t w, uint32_t NT, uint32_t r,
-                                                 uint32_t c, float inv) {
-  for (; w < s.W; w += NT) {
-    iq_store(rq, iq_load<VEC>(rx, r, c, s), inv, w, s.W);
-    iq_step(r, c, s);
+                                                 const InputQuantShape& s, uint32_t w, uint32_t count, uint32_t r,
+                                                 uint32_t c, uint32_t dr, uint32_t dc, float inv) {
+  const uint32_t dw = dr * s.upr + dc;
+  for (uint32_t k = 0; k < count && w < s.W; k++, w += dw) {
+    iq_store(rq, iq_load<VEC>(rx, r, c, s), inv, w);
+    iq_step(r, c, dr, dc, s.upr);
   }
+}
+
+// The units a thread (workgroup b, thread t) owns: U kept ones from
+// b U 512 + t, 512 apart, then the remaining ones from G U 512 + b 512 + t,
+// G 512 apart.
+__device__ __forceinline__ uint32_t iq_kept0(uint32_t b, uint32_t t, int U) { return b * (uint32_t)U * 512u + t; }
+__device__ __forceinline__ uint32_t iq_rest0(uint32_t b, uint32_t t, int U, uint32_t G) {
+  return G * (uint32_t)U * 512u + b * 512u + t;
 }
 
 template <bool VEC, int U>
@@ -534,18 +550,22 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
                                                                    SlotClear clear) {
   using namespace iq;
   constexpr int KL = lds_units(U), KR = U - KL;
-  static_assert(KR <= kMaxRegUnits && (KL == 0 || KR >= kFirst), "unit split");
-  // one LDS array: the LDS units as [KL][kThreads] 16-byte words, 16 words
-  // of block state, then the finisher's list of deferred workgroups
+  static_assert(KR <= kMaxRegUnits && (KL == 0 || KR >= kFirst) && (KL == 0 || KL % 2 == 1), "unit split");
+  // one LDS array: the LDS units as [kThreads][KL] 16-byte words (one
+  // address register per thread, immediate offsets; KL is odd, so a wave's
+  // 16-byte accesses spread over all banks), 16 words of block state, then
+  // the finisher's list of deferred workgroups
   constexpr int kListWords = (int)rqk::kMaxGrid;
   __shared__ __attribute__((aligned(16))) v4f lds[KL * kThreads + 4 + kListWords / 4];
   uint32_t* const blk = reinterpret_cast<uint32_t*>(lds + KL * kThreads);  // [0] flag, [1] count, [2..] wave maxima
   clear_slots(clear);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
-  const uint32_t NT = (uint32_t)G * kThreads, gtid = (uint32_t)b * kThreads + (uint32_t)tid;
-  const __amdgpu_buffer_rsrc_t rx = bounded_rsrc(x), rq = bounded_rsrc(q);
-  const uint32_t r0 = gtid / sh.upr, c0 = gtid - r0 * sh.upr;
+  static_assert(kThreads == 512, "unit layout");
+  const uint32_t w0 = iq_kept0((uint32_t)b, (uint32_t)tid, U);
+  const __amdgpu_buffer_rsrc_t rx = bounded_rsrc(x);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(q, 0, (int)(sh.W * 4u), 0x00020000);
+  const uint32_t r0 = w0 / sh.upr, c0 = w0 - r0 * sh.upr;
 
   // Pass 1: read every unit once (units past the operand have r >= Mpad >=
   // M and read as zeros).  Units 0 .. KL-1 of the thread go to LDS, the next
@@ -561,31 +581,35 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
 #pragma unroll
     for (int j = 0; j < KL; j++) {
       part[j] = iq_load<VEC>(rx, r, c, sh);
-      iq_step(r, c, sh);
+      iq_step(r, c, sh.kr, sh.kc, sh.upr);
     }
 #pragma unroll
     for (int j = 0; j < kFirst; j++) {
       keep[j] = iq_load<VEC>(rx, r, c, sh);
-      iq_step(r, c, sh);
+      iq_step(r, c, sh.kr, sh.kc, sh.upr);
     }
 #pragma unroll
     for (int j = 0; j < KL; j++) {
       m = iq_absmax(m, part[j]);
-      lds[j * kThreads + tid] = part[j];
+      lds[tid * KL + j] = part[j];
     }
   }
 #pragma unroll
   for (int j = KL > 0 ? kFirst : 0; j < KR; j++) {
     keep[j] = iq_load<VEC>(rx, r, c, sh);
-    iq_step(r, c, sh);
+    iq_step(r, c, sh.kr, sh.kc, sh.upr);
   }
 #pragma unroll
   for (int j = 0; j < KR; j++) m = iq_absmax(m, keep[j]);
-  const uint32_t rest_r = r, rest_c = c;
-  const uint32_t rest_w = gtid + (uint32_t)U * NT;
+  // the remaining units (an input larger than the grid keeps)
+  const uint32_t NT = (uint32_t)G * kThreads;
+  const uint32_t rest_w = iq_rest0((uint32_t)b, (uint32_t)tid, U, (uint32_t)G);
+  const uint32_t rest_r = rest_w / sh.upr, rest_c = rest_w - rest_r * sh.upr;
+  r = rest_r;
+  c = rest_c;
   for (uint32_t w = rest_w; w < sh.W; w += NT) {
     m = iq_absmax(m, iq_load<VEC>(rx, r, c, sh));
-    iq_step(r, c, sh);
+    iq_step(r, c, sh.nr, sh.nc, sh.upr);
   }
   // the workgroup's absmax: one atomic into its partial of the spread slot
   const uint32_t mw = wave_max_u32(rgmath::fbits(m));
@@ -617,10 +641,10 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   const float inv = 1.0f / scale;
   // pass 2: the kept units, then the rest from the input
 #pragma unroll
-  for (int j = 0; j < KL; j++) iq_store(rq, lds[j * kThreads + tid], inv, gtid + (uint32_t)j * NT, sh.W);
+  for (int j = 0; j < KL; j++) iq_store(rq, lds[tid * KL + j], inv, w0 + (uint32_t)j * kThreads);
 #pragma unroll
-  for (int j = 0; j < KR; j++) iq_store(rq, keep[j], inv, gtid + (uint32_t)(KL + j) * NT, sh.W);
-  iq_quantize_from<VEC>(rx, rq, sh, rest_w, NT, rest_r, rest_c, inv);
+  for (int j = 0; j < KR; j++) iq_store(rq, keep[j], inv, w0 + (uint32_t)(KL + j) * kThreads);
+  iq_quantize_from<VEC>(rx, rq, sh, rest_w, ~0u, rest_r, rest_c, sh.nr, sh.nc, inv);
   if (flag != 2) return;
 
   // Finisher: the scale tap, then the units of every deferred workgroup.
@@ -633,9 +657,10 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   const uint32_t tid2 = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 64u +
                         __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   for (int d = 0; d < ndef; d++) {
-    const uint32_t g2 = list[d] * kThreads + tid2;
-    const uint32_t rr = g2 / sh.upr;
-    iq_quantize_from<VEC>(rx, rq, sh, g2, NT, rr, g2 - rr * sh.upr, inv);
+    const uint32_t k0 = iq_kept0(list[d], tid2, U), kr0 = k0 / sh.upr;
+    iq_quantize_from<VEC>(rx, rq, sh, k0, (uint32_t)U, kr0, k0 - kr0 * sh.upr, sh.kr, sh.kc, inv);
+    const uint32_t q0 = iq_rest0(list[d], tid2, U, (uint32_t)G), qr0 = q0 / sh.upr;
+    iq_quantize_from<VEC>(rx, rq, sh, q0, ~0u, qr0, q0 - qr0 * sh.upr, sh.nr, sh.nc, inv);
   }
 }
 
@@ -703,8 +728,9 @@ void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int6
   const bool vec = K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   const IqLaunch lc = input_quant_choice(Mpad, Kpad);
   const int64_t W = Mpad * Kpad / 4, NT = lc.G * iq::kThreads, upr = Kpad / 4;
-  const InputQuantShape sh{(int32_t)M, (int32_t)K, (uint32_t)upr, (uint32_t)W, (uint32_t)(NT / upr),
-                           (uint32_t)(NT % upr)};
+  const InputQuantShape sh{(int32_t)M,          (int32_t)K,          (uint32_t)upr,       (uint32_t)W,
+                           (uint32_t)(iq::kThreads / upr), (uint32_t)(iq::kThreads % upr),
+                           (uint32_t)(NT / upr), (uint32_t)(NT % upr)};
   if (vec)
     launch_iq_u<true>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, clear, s);
   else

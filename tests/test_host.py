@@ -204,6 +204,10 @@ def test_fast_quantizer_matches_quantize_rule(tmp_path):
     out = subprocess.run([str(exe), stride, "0", str(min(8, os.cpu_count() or 1))], check=True, capture_output=True,
                          text=True).stdout.split()
     assert int(out[0]) >= (1 << 32) // 13 and int(out[1]) == 0, f"first mismatch at 0x{out[2]}"
+    # the clamp-free form: |v * inv| < 127.5 for every finite absmax (all of them)
+    out = subprocess.run([str(exe), "1", "0", str(min(8, os.cpu_count() or 1)), "bound"], check=True,
+                         capture_output=True, text=True).stdout.split()
+    assert int(out[0]) == 0x7f800000 and int(out[1]) == 0, f"bound fails at absmax 0x{out[2]}"
 
 
 def test_program_create_fails_loudly_without_gpu(rg):
