@@ -1198,15 +1198,25 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
 // (those are a few KiB and stay in L1), sums them (INT8: sdot4, exact; FP16:
 // fdot2, FP32: FMA, in gemv_kernel's order), and the wave's N sums are
 // reduce-scattered as in gemv_kernel before the fused epilogue.  Kpad is in
-// bytes.
-template <int NN, int MODE>
+// bytes.  With XQ (INT8) A is the f32 input [M, xk] (xk % 4 == 0, 16-byte
+// aligned rows), quantized as it is read (QuantTensor::from_f32 with the
+// spread slot's scale, quantize.rs:18-24): each value is read once, so the
+// separate quantize pass over it is gone; q_out (capture) receives the i8
+// operand [M, Kpad] and scale_out the scale.
+template <int NN, int MODE, bool XQ = false>
 __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
-                                                          int64_t M, int64_t N, int64_t Kpad, Epilogue ep) {
+                                                          int64_t M, int64_t N, int64_t Kpad, Epilogue ep, int64_t xk,
+                                                          int8_t* q_out, float* scale_out) {
   constexpr int S = pow2_at_least(NN);
   constexpr int SPREAD = 64 / S;
   const int lane = threadIdx.x & 63;
-  float cs = 1.0f;
-  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  float cs = 1.0f, inv = 0.0f;
+  if constexpr (MODE == kModeI8) {
+    const float sa = tensor_scale(ep.absmax_in);
+    cs = sa * ep.w_scale;
+    inv = 1.0f / sa;
+    if (XQ && scale_out && blockIdx.x == 0 && threadIdx.x == 0) *scale_out = sa;
+  }
   const int sidx = lane / SPREAD;
   const bool owner = (lane % SPREAD) == 0 && sidx < N;
   const float bias_v = ep.bias[sidx < N ? sidx : N - 1];
@@ -1221,8 +1231,27 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restri
       const int64_t k = t * 1024 + lane * 16;
       const bool ok = k < Kpad;
       const int64_t kk = ok ? k : klast;
-      const v4i al = *reinterpret_cast<const v4i*>(A + row * Kpad + kk);
-      const v4i av = ok ? al : v4i{0, 0, 0, 0};
+      v4i av;
+      if constexpr (XQ) {
+        // 16 inputs of the row from k on: zeros past its xk values
+        const float* xr = reinterpret_cast<const float*>(A) + row * xk;
+        v4f f[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          f[g] = k + 4 * g < xk ? *reinterpret_cast<const v4f*>(xr + k + 4 * g) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(f[g][0] * inv) & 0xffu;
+          const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(f[g][1] * inv) & 0xffu;
+          const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(f[g][2] * inv) & 0xffu;
+          const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(f[g][3] * inv) & 0xffu;
+          av[g] = (int32_t)(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24));
+        }
+        if (q_out && ok) *reinterpret_cast<v4i*>(q_out + row * Kpad + k) = av;
+      } else {
+        const v4i al = *reinterpret_cast<const v4i*>(A + row * Kpad + kk);
+        av = ok ? al : v4i{0, 0, 0, 0};
+      }
 #pragma unroll
       for (int n = 0; n < NN; n++) {
         const v4i w = *reinterpret_cast<const v4i*>(B + (int64_t)n * Kpad + kk);
@@ -1282,24 +1311,37 @@ __global__ __launch_bounds__(256) void gemm_narrow_kernel(const int8_t* __restri
   }
 }
 
-template <int MODE>
+template <int MODE, bool XQ = false>
 static void launch_gemm_narrow_t(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad_bytes,
-                                 const Epilogue& ep, hipStream_t s) {
+                                 const Epilogue& ep, hipStream_t s, int64_t xk = 0, int8_t* q_out = nullptr,
+                                 float* scale_out = nullptr) {
   if (N <= 0 || N > kNarrowMaxN || Kpad_bytes % 16 || Kpad_bytes <= 0)
     throw std::logic_error("narrow GEMM: N must be 1..16 and K padded to 16 bytes");
   if (M <= 0) return;
   const int64_t blocks = std::min<int64_t>((M + 3) / 4, 8192);
   if (N <= 4)
-    RG_LAUNCH((gemm_narrow_kernel<4, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
+    RG_LAUNCH((gemm_narrow_kernel<4, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep,
+              xk, q_out, scale_out);
   else if (N <= 8)
-    RG_LAUNCH((gemm_narrow_kernel<8, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
+    RG_LAUNCH((gemm_narrow_kernel<8, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep,
+              xk, q_out, scale_out);
   else
-    RG_LAUNCH((gemm_narrow_kernel<16, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep);
+    RG_LAUNCH((gemm_narrow_kernel<16, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep,
+              xk, q_out, scale_out);
 }
 
 void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
                         hipStream_t s) {
   launch_gemm_narrow_t<kModeI8>(A, B, M, N, Kpad, ep, s);
+}
+
+bool gemm_narrow_xq_supported(int64_t K, int64_t Kpad) { return K > 0 && K % 4 == 0 && K <= Kpad && Kpad % 16 == 0; }
+
+void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t K, int64_t Kpad,
+                           const Epilogue& ep, int8_t* q_out, float* scale_out, hipStream_t s) {
+  if (!gemm_narrow_xq_supported(K, Kpad) || (reinterpret_cast<uintptr_t>(x) & 15) || !ep.absmax_in)
+    throw std::logic_error("narrow GEMM: the quantizing form needs K % 4 == 0, an aligned input and a slot");
+  launch_gemm_narrow_t<kModeI8, true>(reinterpret_cast<const int8_t*>(x), B, M, N, Kpad, ep, s, K, q_out, scale_out);
 }
 
 void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
@@ -1340,7 +1382,15 @@ void launch_gemv_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N,
 // (grid.y) x TN pixels (grid.x); wave w owns pixels [p0 + w TN/4, +TN/4).
 // LDS holds the block's weights (row stride Kpad + 16) and the input rows its
 // pixels read, zero padded and channel-last: band[r][x][c], r < R,
-// x < W + 2 pad, c < cp.  A 16-byte K chunk of an im2col column is then 16
+// x < W + 2 pad, c < cp.  With XF the input is the f32 image and the band
+// is filled with its quantized values (quantize_into's per-image scale,
+// quantize.rs:27-35, from the image's absmax slot): a thread quantizes 4
+// channels of one pixel and writes them as one 32-bit word, and no i8 image
+// exists in memory.  With self_absmax (the run's first conv, an image of at
+// most kConvSelfAbsmaxMax floats whose every pixel a window reads) each
+// block also measures the absmax of its whole image first, so no absmax
+// pass runs before the conv; block (0, 0) of each image publishes it in the
+// image's slot (read only after this kernel: the capture tap).  A 16-byte K chunk of an im2col column is then 16
 // channels of one tap (cp >= 16: one ds_read_b128) or 4 channels of 4 taps
 // (cp == 4: four ds_read_b32); taps past k*k read a zero block.  Outputs are
 // stored straight from the accumulators (16 consecutive pixels per store).
@@ -1394,9 +1444,17 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
   }
 }
 
-template <int TM, int TN, bool CP4>
+constexpr int64_t kConvSelfAbsmaxMax = 16384;
+
+// Publishes a block-measured per-image absmax in the image's slot (zeroed
+// at the start of the run, read only after the kernel).
+__device__ __forceinline__ void ep_absmax_publish(const uint32_t* slots, int b, uint32_t v) {
+  const_cast<uint32_t*>(slots)[b] = v;
+}
+
+template <int TM, int TN, bool CP4, bool XF = false>
 __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ Wt,
-                                                        ConvShape cs, Epilogue ep) {
+                                                        ConvShape cs, Epilogue ep, int self_absmax, SlotClear clear) {
   extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
   constexpr int WTN = TN / 4, FM = TM / 16, FN = WTN / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1411,6 +1469,41 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
   const int band_bytes = R * Wp * cp;
   int8_t* const zero16 = band + ((band_bytes + 15) & ~15);
 
+  // The f32 input's first band batch (see step 2), loaded up front.
+  const int iy_base = oy0 * st - pad;
+  float img_scale = 0.0f;
+  constexpr int BATCH = 8;
+  float v[BATCH][4];  // unused (and removed) in the i8 form
+  int dst[BATCH];
+  const float* imgf = reinterpret_cast<const float*>(xq) + (int64_t)b * C * H * W;
+  const int per_g = R * W, total = (cp / 4) * per_g;  // channel groups of 4 (cp is 4 or a multiple of 16)
+  auto load_batch = [&](int e0) {
+#pragma unroll
+    for (int u = 0; u < BATCH; u++) {
+      const int e = e0 + u * 256;
+      const int g = e / per_g, t = e - g * per_g, r = t / W, x = t - r * W;
+      const int iy = iy_base + r;
+      const bool ok = e < total && iy >= 0 && iy < H;
+      dst[u] = ok ? (r * Wp + x + pad) * cp + 4 * g : -1;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int c = 4 * g + q;
+        v[u][q] = ok && c < C ? imgf[((int64_t)c * H + iy) * W + x] : 0.0f;
+      }
+    }
+  };
+  auto store_batch = [&](float inv) {
+#pragma unroll
+    for (int u = 0; u < BATCH; u++) {
+      if (dst[u] < 0) continue;
+      uint32_t word = 0;
+#pragma unroll
+      for (int q = 0; q < 4; q++) word |= ((uint32_t)rgmath::quantize_rz(v[u][q] * inv) & 0xffu) << (8 * q);
+      *reinterpret_cast<uint32_t*>(band + dst[u]) = word;
+    }
+  };
+  if constexpr (XF) load_batch(tid);
+
   // 1. zero the band and the zero block; copy this block's weights.
   for (int i = tid; i <= (band_bytes + 15) / 16; i += 256) *reinterpret_cast<v4i*>(band + 16 * i) = v4i{0, 0, 0, 0};
   const int kc = KP / 16;
@@ -1420,10 +1513,48 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
         *reinterpret_cast<const v4i*>(Wt + (int64_t)(o0 + row) * KP + c16 * 16);
   }
   __syncthreads();
-  // 2. input rows iy = oy0*st - pad + r of every channel, channel-last.
-  const int8_t* img = xq + (int64_t)b * C * H * W;
-  const int iy_base = oy0 * st - pad;
-  if ((W & 3) == 0) {
+  // 2. input rows iy = oy0*st - pad + r of every channel, channel-last.  The
+  // f32 input: with self_absmax the image's absmax first (its loads overlap
+  // the first batch's), then the batches are quantized into the band.
+  if constexpr (XF) {
+    if (self_absmax) {
+      clear_slots(clear);
+      float m = 0.0f;  // NaN ignored, like f32::max
+      const int n = C * H * W;
+      if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(imgf) & 15) == 0) {
+        const float4* f4 = reinterpret_cast<const float4*>(imgf);
+        const int n4 = n >> 2;
+        for (int e = tid; e < n4; e += 4 * 256) {
+          float4 w4[4];
+#pragma unroll
+          for (int u = 0; u < 4; u++) w4[u] = e + u * 256 < n4 ? f4[e + u * 256] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(w4[u].x)), __builtin_fabsf(w4[u].y));
+            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(w4[u].z)), __builtin_fabsf(w4[u].w));
+          }
+        }
+      } else {
+        for (int e = tid; e < n; e += 256) m = __builtin_fmaxf(m, __builtin_fabsf(imgf[e]));
+      }
+      __shared__ uint32_t red[4];
+      const uint32_t w = wave_max_u32(rgmath::fbits(m));
+      if (lane == 0) red[wave] = w;
+      __syncthreads();
+      const uint32_t t = max(max(red[0], red[1]), max(red[2], red[3]));
+      if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) ep_absmax_publish(ep.absmax_in, b, t);
+      img_scale = rgmath::scale_from_absmax(rgmath::bitsf(t));
+    } else {
+      img_scale = slot_scale(ep.absmax_in + b);
+    }
+    const float inv = 1.0f / img_scale;
+    store_batch(inv);
+    for (int e0 = tid + 256 * BATCH; e0 < total; e0 += 256 * BATCH) {
+      load_batch(e0);
+      store_batch(inv);
+    }
+  } else if ((W & 3) == 0) {
+    const int8_t* img = xq + (int64_t)b * C * H * W;
     const int wq = W >> 2, per_c = R * wq;
     for (int e = tid; e < C * per_c; e += 256) {
       const int c = e / per_c, t = e - c * per_c, r = t / wq, x = (t - r * wq) * 4;
@@ -1438,6 +1569,7 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
       }
     }
   } else {
+    const int8_t* img = xq + (int64_t)b * C * H * W;
     const int per_c = R * W;
     for (int e = tid; e < C * per_c; e += 256) {
       const int c = e / per_c, t = e - c * per_c, r = t / W, x = t - r * W;
@@ -1493,7 +1625,11 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
       for (int j = 0; j < FN; j++)
         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
   }
-  const float csc = slot_scale(ep.absmax_in + b) * ep.w_scale;
+  float csc;
+  if constexpr (XF)
+    csc = img_scale * ep.w_scale;
+  else
+    csc = slot_scale(ep.absmax_in + b) * ep.w_scale;
   switch (ep.act) {
     case rgmath::ACT_RELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_RELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
     case rgmath::ACT_SIGMOID: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SIGMOID>(acc, cs, ep, b, o0, pix, csc, lane); break;
@@ -1597,12 +1733,14 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
   epilogue_tile<TM, TN, CLD, true>(Cs, tc, csc, ep);
 }
 
-template <int TM, int TN, bool CP4>
-static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {
+template <int TM, int TN, bool CP4, bool XF>
+static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
+                          int self_absmax = 0, SlotClear clear = SlotClear{}) {
   const ConvBand g = conv_band_geom(cs, TM, TN);
-  constexpr int kMaxLds = 160 * 1024;
+  constexpr int kStatic = XF ? 64 : 0;  // the f32 form's few words of static LDS
+  constexpr int kMaxLds = 160 * 1024 - kStatic;
   if (g.lds_bytes > kMaxLds) return false;
-  const void* fn = reinterpret_cast<const void*>(&conv_band_kernel<TM, TN, CP4>);
+  const void* fn = reinterpret_cast<const void*>(&conv_band_kernel<TM, TN, CP4, XF>);
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds) != hipSuccess) return false;
@@ -1610,15 +1748,34 @@ static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& c
   }
   const int64_t L = cs.OH * cs.OW;
   dim3 grid((unsigned)((L + TN - 1) / TN), (unsigned)(cs.Opad / TM), (unsigned)cs.n);
-  RG_LAUNCH((conv_band_kernel<TM, TN, CP4>), grid, dim3(256), (unsigned)g.lds_bytes, s, xq, Wq, cs, ep);
+  RG_LAUNCH((conv_band_kernel<TM, TN, CP4, XF>), grid, dim3(256), (unsigned)g.lds_bytes, s, xq, Wq, cs, ep,
+            self_absmax, clear);
   return true;
 }
 
-template <int TM, bool CP4>
+template <int TM, bool CP4, bool XF>
 static bool try_conv_band_tn(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
-                             hipStream_t s) {
-  return try_conv_band<TM, 256, CP4>(xq, Wq, cs, ep, s) || try_conv_band<TM, 128, CP4>(xq, Wq, cs, ep, s) ||
-         try_conv_band<TM, 64, CP4>(xq, Wq, cs, ep, s);
+                             hipStream_t s, int self_absmax = 0, SlotClear clear = SlotClear{}) {
+  return try_conv_band<TM, 256, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear) ||
+         try_conv_band<TM, 128, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear) ||
+         try_conv_band<TM, 64, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear);
+}
+
+bool conv_self_absmax_supported(const ConvShape& cs) { return cs.C * cs.H * cs.W <= kConvSelfAbsmaxMax; }
+
+bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
+                       bool self_absmax, SlotClear clear) {
+  if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31))
+    throw std::logic_error("conv: shape too large for the kernel's indexing");
+  if (self_absmax && !conv_self_absmax_supported(cs)) throw std::logic_error("conv: image too large for self_absmax");
+  const int8_t* xb = reinterpret_cast<const int8_t*>(x);
+  const bool cp4 = cs.cp == 4;
+  const int sa = self_absmax ? 1 : 0;
+  if (cs.Opad % 64 == 0)
+    return cp4 ? try_conv_band_tn<64, true, true>(xb, Wq, cs, ep, s, sa, clear)
+               : try_conv_band_tn<64, false, true>(xb, Wq, cs, ep, s, sa, clear);
+  return cp4 ? try_conv_band_tn<32, true, true>(xb, Wq, cs, ep, s, sa, clear)
+             : try_conv_band_tn<32, false, true>(xb, Wq, cs, ep, s, sa, clear);
 }
 
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {
@@ -1627,9 +1784,9 @@ void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const 
   const bool cp4 = cs.cp == 4;
   bool done;
   if (cs.Opad % 64 == 0)
-    done = cp4 ? try_conv_band_tn<64, true>(xq, Wq, cs, ep, s) : try_conv_band_tn<64, false>(xq, Wq, cs, ep, s);
+    done = cp4 ? try_conv_band_tn<64, true, false>(xq, Wq, cs, ep, s) : try_conv_band_tn<64, false, false>(xq, Wq, cs, ep, s);
   else
-    done = cp4 ? try_conv_band_tn<32, true>(xq, Wq, cs, ep, s) : try_conv_band_tn<32, false>(xq, Wq, cs, ep, s);
+    done = cp4 ? try_conv_band_tn<32, true, false>(xq, Wq, cs, ep, s) : try_conv_band_tn<32, false, false>(xq, Wq, cs, ep, s);
   if (done) return;
   constexpr int TN = 128;
   const int64_t L = cs.OH * cs.OW;

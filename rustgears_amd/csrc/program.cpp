@@ -1051,7 +1051,14 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         }
         uint32_t* slot = slots + pl.slot_base;
         int8_t* const qa = pl.q_in ? plan.q_alt.as<int8_t>() : q;
-        if (pl.iq_sync_base >= 0) {
+        // A narrow GEMM after a producer that emitted the absmax quantizes
+        // its input as it reads it (an unaligned input takes quant_rows).
+        const bool narrow_xq = !pl.gemv && op.out_f <= kNarrowMaxN && !pl.explicit_absmax && !pl.q_ready &&
+                               pl.rows > 0 && gemm_narrow_xq_supported(op.in_f, op.Kpad) &&
+                               (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+        if (narrow_xq) {
+          // nothing before the GEMM
+        } else if (pl.iq_sync_base >= 0) {
           launch_input_quant(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base,
                              slots + pl.iq_sync_base, plan.spin_limit, clear, s);
           first_launched();
@@ -1086,6 +1093,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             launch_gemm_requant(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, rq, s);
           } else if (pl.gemv) {
             launch_gemv(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+          } else if (narrow_xq) {
+            launch_gemm_narrow_xq(in, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.in_f, op.Kpad, ep, cap ? qa : nullptr,
+                                  cap ? scales + pl.scale_base : nullptr, s);
           } else if (op.out_f <= kNarrowMaxN) {
             launch_gemm_narrow(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Kpad, ep, s);
           } else {
@@ -1136,7 +1146,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         }
         uint32_t* sl = slots + pl.slot_base;
         const int64_t per = c.C * c.H * c.W;
-        if (pl.explicit_absmax) {
+        // a small, fully covered first image: the conv measures its absmax itself
+        const bool self_absmax = pl.explicit_absmax && pl.full_cov && conv_self_absmax_supported(c);
+        if (pl.explicit_absmax && !self_absmax) {
           const uint8_t* mk = plan.masks.as<uint8_t>() + pl.mask_off;
           if (pl.full_cov)
             launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s, clear);
@@ -1144,7 +1156,6 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             launch_absmax(in, per, c.n, sl, false, mk, mk + c.H, c.H, c.W, s, clear);
           first_launched();
         }
-        launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
         Epilogue ep;
         ep.bias = op.d_bias.as<float>();
         ep.act = op.act;
@@ -1155,8 +1166,30 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         ep.absmax_out = emit;
         ep.absmax_out_per_image = pl.emit_per_image;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
+        // The conv quantizes the f32 image into its LDS band itself; the
+        // separate i8 image is made only for the capture tap (after the conv
+        // when the conv measures the absmax), or when the band does not fit
+        // in LDS.
+        if (cap && !self_absmax) launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
         pre = launch_events_used();
-        if (c.n > 0 && c.OH * c.OW > 0) launch_conv(q, op.d_w.as<int8_t>(), c, ep, s);
+        bool fused = false;
+        if (c.n > 0 && c.OH * c.OW > 0) {
+          fused = launch_conv_f32in(in, op.d_w.as<int8_t>(), c, ep, s, self_absmax, clear);
+          if (self_absmax && fused) first_launched();
+          if (!fused) {
+            if (self_absmax) {  // the band does not fit: the absmax pass after all
+              launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s, clear);
+              first_launched();
+            }
+            if (!cap || self_absmax) launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
+            pre = launch_events_used();
+            launch_conv(q, op.d_w.as<int8_t>(), c, ep, s);
+          }
+        } else if (self_absmax) {
+          launch_absmax(in, per, c.n, sl, false, nullptr, nullptr, 0, 0, s, clear);
+          first_launched();
+        }
+        if (cap && self_absmax && fused) launch_quant_images(in, per, c.n, sl, q, scales + pl.scale_base, s);
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, q, (size_t)pl.in_len, hipMemcpyDeviceToDevice, s));
         break;
       }

@@ -151,6 +151,13 @@ void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int6
 constexpr int64_t kNarrowMaxN = 16;
 void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Kpad, const Epilogue& ep,
                         hipStream_t s);
+// The same reading the f32 input x [M, K] and quantizing it as it is read,
+// with the scale of the spread slot ep.absmax_in (a producer emitted it);
+// q_out / scale_out (nullable) receive the i8 operand [M, Kpad] and the
+// scale (capture).
+bool gemm_narrow_xq_supported(int64_t K, int64_t Kpad);
+void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t K, int64_t Kpad,
+                           const Epilogue& ep, int8_t* q_out, float* scale_out, hipStream_t s);
 void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
                             const Epilogue& ep, hipStream_t s);
 void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Kpad_f, const Epilogue& ep,
@@ -171,6 +178,15 @@ inline int64_t conv_cp(int64_t C) { return C <= 4 ? 4 : round_up(C, 16); }
 inline int64_t conv_kpad(int64_t C, int64_t k) { return round_up(k * k * conv_cp(C), 64); }
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
                  hipStream_t s);
+// The same conv reading the f32 image and quantizing its band in LDS with
+// the image's scale (ep.absmax_in, one slot per image); false when the
+// band does not fit in LDS (then quantize the image and use launch_conv).
+// With self_absmax (conv_self_absmax_supported: small, fully covered
+// images) the kernel measures each image's absmax itself, publishes it in
+// ep.absmax_in, and zeroes `clear` (the run's first kernel).
+bool conv_self_absmax_supported(const ConvShape& cs);
+bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
+                       bool self_absmax = false, SlotClear clear = SlotClear{});
 
 // ---- NpuPrecision::Fp16 ----------------------------------------------------
 // GEMM on IEEE binary16 operands (A [Mpad, Kpad_h], B [Npad, Kpad_h], Kpad_h a

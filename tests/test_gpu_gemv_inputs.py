@@ -1,0 +1,88 @@
+"""The inputs of the M <= 8 GEMV (QuantTensor::from_f32, quantize.rs:18-24,
+at npu.rs:312, then quantize.rs:93-118 with the rows streamed once).
+
+Bit for bit against the oracle, capture taps included:
+
+* every M from 1 to 8, with the scale from the input's own absmax (the
+  run's first Linear: the one-pass input quantization, a single workgroup
+  at these sizes) and from the producer's absmax slot (a GEMV after a GEMV);
+* inputs holding NaN, +-inf and the absmax at the last column;
+* K % 4 != 0 (element loads), a long K (the input larger than one
+  workgroup keeps), and an input pointer that is not 16-byte aligned
+  (run_device on an offset buffer).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact_f32
+from test_gpu_parity import check_against_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _mlp(rg, dims, seed, act="gelu"):
+    from rustgears_amd import nn
+    rg.manual_seed(seed)
+    acts = {"tanh": nn.Tanh, "relu": nn.Relu, "gelu": nn.Gelu}
+    m = nn.Sequential()
+    for i, (a, b) in enumerate(zip(dims[:-1], dims[1:])):
+        m.add(nn.Linear(a, b))
+        if i + 2 < len(dims):
+            m.add(acts[act]())
+    return m.export()
+
+
+@pytest.mark.parametrize("rows", list(range(1, 9)))
+def test_gemv_every_m(rg, ref, rows):
+    layers = _mlp(rg, [1000, 3000, 700], seed=50 + rows)
+    x = rg.randn([rows, 1000])
+    check_against_oracle(rg, ref, layers, x, f"gemv M={rows}")
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y = sess.run(x)
+    sess.close()
+    assert_bitexact_f32(y, ref.RefProgram(layers).run(x), f"gemv M={rows} (no capture)")
+
+
+def test_gemv_special_values(rg, ref):
+    layers = _mlp(rg, [512, 1024, 64], seed=7, act="relu")
+    x = rg.randn([4, 512])
+    x[0, 3] = np.nan
+    x[1, 511] = -1234.5  # the absmax, at the last column
+    check_against_oracle(rg, ref, layers, x, "gemv NaN / absmax last column")
+    x2 = x.copy()
+    x2[2, 100] = np.inf
+    x2[3, 7] = -np.inf
+    check_against_oracle(rg, ref, layers, x2, "gemv inf")
+
+
+@pytest.mark.parametrize("dims,rows", [([333, 600, 40], 3), ([20000, 1024, 64], 8)], ids=["K%4", "long K"])
+def test_gemv_odd_and_long_rows(rg, ref, dims, rows):
+    layers = _mlp(rg, dims, seed=rows + dims[0])
+    check_against_oracle(rg, ref, layers, rg.randn([rows, dims[0]]), f"gemv {dims} M={rows}")
+
+
+def test_unaligned_device_input(rg, ref):
+    from rustgears_amd.inference import DeviceBuffer
+    layers = _mlp(rg, [1024, 2048, 256], seed=3)
+    x = rg.randn([2, 1024])
+    want = ref.RefProgram(layers).run(x)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    buf = DeviceBuffer(x.nbytes + 16)
+    padded = np.zeros(x.size + 4, np.float32)
+    padded[1:1 + x.size] = x.reshape(-1)
+    buf.upload(padded)
+
+    class Offset:  # the same allocation, 4 bytes in
+        ptr = buf.ptr + 4
+        nbytes = x.nbytes
+
+    d_y = DeviceBuffer(2 * 256 * 4)
+    for src, what in ((Offset, "unaligned"),):
+        assert sess.run_device(src, x.shape, d_y) == (2, 256)
+        sess.synchronize()
+        assert_bitexact_f32(d_y.download((2, 256)), want, f"gemv {what} input")
+    d_x = DeviceBuffer.from_array(x)
+    sess.run_device(d_x, x.shape, d_y)
+    sess.synchronize()
+    assert_bitexact_f32(d_y.download((2, 256)), want, "gemv aligned input")
+    sess.close()
