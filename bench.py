@@ -202,13 +202,54 @@ def cpu_baseline(name, layers, x, target_s: float, prec="int8"):
                       f"like rayon (quantize.rs:104), effective parallelism min(rows, threads) = {eff}"}
 
 
+def mfma_peak(rg, args):
+    """The sustained i8 MFMA rate the GEMMs are measured against: the
+    register-only probe kernel (kernels.hip mfma_peak_kernel, 8 waves per CU,
+    32 independent v_mfma_i32_16x16x64_i8 per round, the large GEMM's inner
+    loop without its memory traffic) on random and on all-zero operand bytes,
+    for launches of about 1, 5 and 20 ms; `steps` launches each, the
+    median reported.  The rate under random data is what bounds the S
+    GEMM's K loop; the zero-operand rate shows the data-dependent power
+    limit."""
+    import ctypes
+    from rustgears_amd import _native as N
+    peak = 5000.0
+    res = {}
+    for mode, rnd in (("random", 1), ("zero", 0)):
+        res[mode] = {}
+        for iters in (500, 2_500, 10_000):
+            rates, mss = [], []
+            for k in range(args.warmup + args.steps):
+                ms, tops = ctypes.c_double(), ctypes.c_double()
+                N.check(N.lib().rgnpu_probe_mfma_rate(0, iters, rnd, ctypes.byref(ms), ctypes.byref(tops)))
+                if k >= args.warmup:
+                    rates.append(tops.value)
+                    mss.append(ms.value)
+            res[mode][iters] = (float(np.median(rates)), float(np.median(mss)))
+            print(f"# mfma probe {mode:6s} iters {iters:6d}: {res[mode][iters][1]:7.3f} ms "
+                  f"{res[mode][iters][0]:8.1f} TOPS ({100 * res[mode][iters][0] / peak:.1f}% of {peak:.0f})",
+                  file=sys.stderr, flush=True)
+    long_iters = 10_000
+    v = res["random"][long_iters][0]
+    line = {"metric": "sustained i8 MFMA rate (register-only probe, random operands)", "value": round(v, 1),
+            "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(res["random"][long_iters][1], 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "i8", "data": "synthetic: SplitMix64 operand bytes / all-zero bytes",
+            "config": {"workload": "mfma_peak", "kernel": "mfma_peak_kernel", "waves_per_cu": 8,
+                       "mfma": "v_mfma_i32_16x16x64_i8"},
+            "frac_of_peak": round(v / peak, 4), "peak": peak,
+            "by_launch": {mode: {str(it): {"tops": round(r[0], 1), "ms": round(r[1], 4)} for it, r in d.items()}
+                          for mode, d in res.items()}}
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="linear_stack",
-                    choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart", "copy"])
+                    choices=["linear_stack", "gemv", "deep_mlp", "cnn", "quickstart", "copy", "mfma_peak"])
     ap.add_argument("--batch", type=int, default=1, help="gemv batch (1 or 8)")
     ap.add_argument("--gemv-act", default="silu", choices=["silu", "relu"],
                     help="activation after the first gemv layer (relu: the twin the reference can express)")
@@ -225,6 +266,10 @@ def main():
         sys.exit(2)
 
     import rustgears_amd as rg
+
+    if args.workload == "mfma_peak":
+        mfma_peak(rg, args)
+        return
 
     t_setup = time.perf_counter()
     layers, x, config = build_workload(args.workload, args.batch, args.stack_act, args.gemv_act)

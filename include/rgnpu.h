@@ -236,6 +236,14 @@ void rgnpu_fill_uniform_range(float* out, int64_t n, float lo, float hi); /* Ten
 void rgnpu_fill_normal(float* out, int64_t n);                           /* Tensor::randn */
 
 /* ---- device buffers for callers without their own allocator -------------- */
+/* Sustained i8 MFMA rate of the device: one launch of a register-only loop
+ * of independent v_mfma_i32_16x16x64_i8 (8 waves per CU, `iters` rounds of
+ * 32 per wave, no memory traffic in the loop) on random or all-zero operand
+ * bytes, timed with HIP events.  Writes the elapsed ms and the rate in
+ * TOPS (2 ops per MAC).  No counterpart in the reference: it measures the
+ * ceiling that the GEMM kernels' MFMA utilization is compared against. */
+int rgnpu_probe_mfma_rate(int32_t device, int64_t iters, int32_t random_operands, double* ms, double* tops);
+
 int rgnpu_device_count(int32_t* count);
 int rgnpu_device_alloc(int32_t device, int64_t bytes, void** out);
 int rgnpu_device_free(void* p);

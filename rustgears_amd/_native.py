@@ -101,6 +101,8 @@ SIGNATURES = [
     ("rgnpu_fill_uniform", None, [f32p, ctypes.c_int64]),
     ("rgnpu_fill_uniform_range", None, [f32p, ctypes.c_int64, ctypes.c_float, ctypes.c_float]),
     ("rgnpu_fill_normal", None, [f32p, ctypes.c_int64]),
+    ("rgnpu_probe_mfma_rate", ctypes.c_int, [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                             ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     ("rgnpu_device_count", ctypes.c_int, [i32p]),
     ("rgnpu_device_alloc", ctypes.c_int, [ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(ctypes.c_void_p)]),
     ("rgnpu_device_free", ctypes.c_int, [ctypes.c_void_p]),

@@ -75,6 +75,67 @@ __global__ __launch_bounds__(256) void evict_kernel(const v4i* __restrict__ p, i
   if (x == never) sink[0] = x;
 }
 
+// Sustained MFMA rate: the shape of the large GEMM's inner loop without its
+// memory traffic.  Every wave (8 per CU, 2 per SIMD) holds 8 A and 4 B
+// operand fragments in registers and runs `iters` rounds of 32 independent
+// v_mfma_i32_16x16x64_i8 (accumulators acc[i][j] += a[i] * b[j], 128
+// accumulator registers), with no LDS, barrier or memory access in the loop.
+// The fragments are built from the 256 words at `seed` (random or zero
+// bytes, chosen by the caller).  The accumulators are folded into sink[0]
+// only if they equal `never`, so the work cannot be dropped.
+__global__ __launch_bounds__(512) void mfma_peak_kernel(const int32_t* __restrict__ seed, int64_t iters,
+                                                        int32_t never, int32_t* __restrict__ sink) {
+  const int l = threadIdx.x;
+  v4i a[8], b[4], acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    a[i] = v4i{seed[(l + i) & 255], seed[(l + 3 * i + 1) & 255], seed[(l + 5 * i + 2) & 255],
+               seed[(l + 7 * i + 3) & 255]};
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    b[j] = v4i{seed[(l + 11 * j) & 255], seed[(l + 13 * j + 5) & 255], seed[(l + 17 * j + 6) & 255],
+               seed[(l + 19 * j + 7) & 255]};
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = v4i{0, 0, 0, 0};
+  for (int64_t it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+  int32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) x ^= acc[i][j][0] ^ acc[i][j][1] ^ acc[i][j][2] ^ acc[i][j][3];
+  if (x == never) sink[0] = x;
+}
+
+double probe_mfma_rate(const void* ops, int64_t iters, int32_t* sink, int64_t* macs_out, hipStream_t s) {
+  int dev = 0, cus = 256;
+  (void)hipGetDevice(&dev);
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+  const int64_t blocks = cus;  // one 8-wave workgroup per CU, as the large GEMM
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return -1.0;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return -1.0;
+  }
+  (void)hipEventRecord(e0, s);
+  hipLaunchKernelGGL(mfma_peak_kernel, dim3((unsigned)blocks), dim3(512), 0, s, reinterpret_cast<const int32_t*>(ops),
+                     iters, (int32_t)0x5bd1e995, sink);
+  (void)hipEventRecord(e1, s);
+  float ms = -1.0f;
+  if (hipGetLastError() == hipSuccess && hipEventSynchronize(e1) == hipSuccess) (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *macs_out = blocks * 8 * iters * 32 * (int64_t)(16 * 16 * 64);
+  return ms;
+}
+
 void launch_evict(const void* p, int64_t bytes, uint32_t* sink, hipStream_t s) {
   const int64_t n = bytes / 16;
   if (n <= 0) return;

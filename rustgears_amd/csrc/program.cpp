@@ -1739,6 +1739,35 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
   }
 }
 
+int rgnpu_probe_mfma_rate(int32_t device, int64_t iters, int32_t random_operands, double* ms, double* tops) {
+  RG_API_BEGIN
+  if (!ms || !tops || iters <= 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
+  RG_HIP(hipSetDevice(device));
+  std::vector<uint8_t> host(256 * 16 + 16, 0);
+  if (random_operands) {
+    uint64_t z = 0x9e3779b97f4a7c15ull;  // SplitMix64 stream
+    for (auto& b : host) {
+      z += 0x9e3779b97f4a7c15ull;
+      uint64_t t = z;
+      t = (t ^ (t >> 30)) * 0xbf58476d1ce4e5b9ull;
+      t = (t ^ (t >> 27)) * 0x94d049bb133111ebull;
+      b = (uint8_t)(t ^ (t >> 31));
+    }
+  }
+  DevBuf buf;
+  buf.ensure(host.size());
+  RG_HIP(hipMemcpy(buf.p, host.data(), host.size(), hipMemcpyHostToDevice));
+  hipStream_t s = nullptr;
+  RG_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  int64_t macs = 0;
+  const double t = probe_mfma_rate(buf.p, iters, reinterpret_cast<int32_t*>(buf.as<uint8_t>() + 256 * 16), &macs, s);
+  (void)hipStreamDestroy(s);
+  if (t <= 0) throw Error(RGNPU_ERR_DEVICE, "MFMA probe launch failed");
+  *ms = t;
+  *tops = 2.0 * (double)macs / (t * 1e-3) / 1e12;
+  RG_API_END
+}
+
 int rgnpu_device_count(int32_t* count) {
   RG_API_BEGIN
   int c = 0;

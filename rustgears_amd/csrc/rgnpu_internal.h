@@ -78,6 +78,12 @@ void launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 // Loads the library's kernels on the current device (one empty launch per
 // code object: kernels.hip and requant.hip).
 void load_code_object(hipStream_t s);
+
+// Times one launch of the register-only MFMA probe (kernels.hip): 8 waves
+// per CU, `iters` rounds of 32 i8 16x16x64 MFMAs per wave on operands built
+// from the 256 words at ops.  Returns the elapsed ms (negative on failure)
+// and the MACs performed.
+double probe_mfma_rate(const void* ops, int64_t iters, int32_t* sink, int64_t* macs_out, hipStream_t s);
 void load_requant_code_object(hipStream_t s);
 
 // Device scratch of the allocation-free run entry point (scratch.hip): one

@@ -103,3 +103,14 @@ def test_first_run_of_a_process_is_not_charged_the_code_object_load():
     assert res.returncode == 0, res.stderr[-2000:]
     worst_ns = int(res.stdout.strip().splitlines()[-1])
     assert worst_ns < 2_000_000, f"first run's slowest op took {worst_ns / 1e3:.1f} us"
+
+
+def test_mfma_probe_rate_is_positive_and_below_nominal():
+    """rgnpu_probe_mfma_rate: the register-only MFMA probe (bench.py
+    --workload mfma_peak) runs and reports a rate under the 5.0 POP/s
+    nominal i8 peak (2 ops per MAC), for random and zero operands."""
+    from rustgears_amd import _native as N
+    for rnd in (1, 0):
+        ms, tops = ctypes.c_double(), ctypes.c_double()
+        N.check(N.lib().rgnpu_probe_mfma_rate(0, 200, rnd, ctypes.byref(ms), ctypes.byref(tops)))
+        assert ms.value > 0 and 100.0 < tops.value < 5200.0, (rnd, ms.value, tops.value)
