@@ -78,23 +78,26 @@ def build_workload(name: str, batch: int, stack_act: str = "gelu", gemv_act: str
     raise SystemExit(f"unknown workload {name}")
 
 
-def measured_traffic(workload: str, kernel: str, prec: str = "int8"):
-    """HBM bytes per launch of `kernel` in `workload` from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/hbm_traffic.txt:
-    lines `workload<TAB>kernel label<TAB>bytes`, already scaled by the copy
-    calibration; the workload carries an `@fp16` / `@fp32` suffix for the
-    other precisions, whose op labels can equal the INT8 ones); None when
-    that pair was not profiled."""
+def measured_traffic(workload: str, kernel: str, prec: str = "int8", occurrence: int = 0):
+    """HBM bytes per launch of the `occurrence`-th op labelled `kernel` in
+    `workload` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/hbm_traffic.txt: lines `workload<TAB>op label<TAB>bytes` in op
+    order, already scaled by the copy calibration; the workload carries an
+    `@fp16` / `@fp32` suffix for the other precisions, whose op labels can
+    equal the INT8 ones); None when that op was not profiled."""
     if prec != "int8":
         workload = f"{workload}@{prec}"
     path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
     if not os.path.exists(path):
         return None
+    seen = 0
     with open(path) as f:
         for line in f:
             parts = line.rstrip("\n").split("\t")
             if len(parts) == 3 and parts[0] == workload and parts[1] == kernel:
-                return int(parts[2])
+                if seen == occurrence:
+                    return int(parts[2])
+                seen += 1
     return None
 
 
@@ -113,6 +116,7 @@ def dominant_roofline(name, records, layers, x, workload, prec="int8"):
     r = records[best]
     if r.kernel_ns <= 0:
         return None, best
+    occ = sum(1 for rr in records[:best] if rr.op == r.op)  # ops sharing the label before it
     secs = r.kernel_ns / 1e9
     if name == "gemv":
         # algorithmic bytes of one GEMV launch: weights N*K + f32 bias N +
@@ -124,19 +128,19 @@ def dominant_roofline(name, records, layers, x, workload, prec="int8"):
         byts = eb * li.in_features * li.out_features + 4 * li.out_features + eb * b * li.in_features + 4 * b * li.out_features
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec),
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec, occ),
                 "kernel": r.op, "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     if r.macs == 0:
         # elementwise op (copy calibration): f32 in + f32 out
         byts = 8 * int(np.prod(x.shape))
         ach = byts / secs / 1e9
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec), "kernel": r.op,
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec, occ), "kernel": r.op,
                 "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
     ops = 2 * r.macs
     ach = ops / secs / 1e12
     return {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(ach / peak, 4), "traffic": measured_traffic(workload, r.op, prec), "kernel": r.op,
+            "frac": round(ach / peak, 4), "traffic": measured_traffic(workload, r.op, prec, occ), "kernel": r.op,
             "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
 
 

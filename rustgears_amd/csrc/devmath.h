@@ -52,6 +52,17 @@ RG_HD float fmax_nan_ignoring(float a, float b) {
 // both give +0.0.
 RG_HD float relu(float x) { return x > 0.0f ? x : 0.0f; }
 
+// ---------------------------------------------------------------------------
+// The constants and steps of expm1f / tanhf below restate fdlibm's
+// s_expm1f.c and s_tanhf.c, which carry this notice:
+//   Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//   Developed at SunPro, a Sun Microsystems, Inc. business.
+//   Permission to use, copy, modify, and distribute this
+//   software is freely granted, provided that this notice
+//   is preserved.
+// (float versions by Ian Lance Taylor, Cygnus Support).
+// ---------------------------------------------------------------------------
+
 // fdlibm expm1f.  Branches are kept in the published order; the tanh path
 // only reaches k in {0,-1,-2,-3} (|x|<1) and k in [3,63] (1<=|x|<22).
 RG_HD float expm1f_fdlibm(float x) {
@@ -339,6 +350,13 @@ RG_HD float gelu_fast(float x) {
   const float one_t = 1.0f + tanh_u;
   return h * one_t;
 }
+
+// ---------------------------------------------------------------------------
+// The table, constants and steps of expf below restate the expf of Arm's
+// optimized-routines (as used by glibc's e_expf.c):
+//   Copyright (c) 2017-2018, Arm Limited.
+//   SPDX-License-Identifier: MIT OR Apache-2.0 WITH LLVM-exception
+// ---------------------------------------------------------------------------
 
 // 2^(i/32) table of ARM optimized-routines expf: asuint64(2^(i/32)) - (i<<47).
 #if defined(__HIPCC__)

@@ -64,7 +64,7 @@ def write(name, layers, x):
 
 
 def main():
-    # 1. README quickstart MLP
+    # 1. the quickstart MLP (configs.quickstart, the 4 -> 32 -> 3 example of the reference's USAGE.md)
     model, x = configs.quickstart()
     write("quickstart_mlp", model.export(), x)
 
