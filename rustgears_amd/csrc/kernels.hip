@@ -1252,6 +1252,176 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
   }
 }
 
+// INT8 GEMV on the matrix cores for a few rows (quantize.rs:104-113 with
+// M <= 8): y[m][n] = act(fl(float(sum_k x[m][k] w[n][k]) * cs) + b[n]).
+//
+// The weights stream through LDS: an item is 16 weight rows x one 512-byte
+// K piece (8 KiB), copied by 8 global_load_lds instructions of two 512-byte
+// row pieces each, so every instruction reads whole 128-byte lines.  Each
+// wave owns a two-stage ring and streams its own items (no workgroup barrier
+// in the loop); the next item's copy is issued before the current one is
+// consumed.  v_mfma_i32_16x16x64_i8 takes the weights as A (row n = lane %
+// 16) and the activations as B (column m = lane % 16, zero for m >= M), so
+// D[n][m] is the exact i32 sum; the activation fragments of a piece (8 K
+// steps x 16 bytes per lane) are loaded once per piece and serve every row
+// block of the workgroup.
+//
+// Workgroup g owns row blocks [g NB / G, (g + 1) NB / G) (at most kGmvBlocks)
+// and its 4 waves split K into contiguous ranges of pieces; each wave walks
+// its pieces, and within a piece the row blocks, keeping one accumulator per
+// block.  The waves' partial sums are added in LDS (integer adds: exact in
+// any order), and the workgroup applies the epilogue.
+//
+// LDS swizzle: row r's 16-byte chunk c lands at position c ^ r (the DMA lane
+// that writes position i fetches chunk i ^ r), so the 16 rows of a fragment
+// read hit 16 different bank groups.
+namespace gmv {
+constexpr int kWaves = 4;
+constexpr int kPiece = 512;                // K bytes per piece
+constexpr int kItem = 16 * kPiece;         // 16 rows x one piece
+constexpr int kDma = kItem / 1024;         // copy instructions per item
+constexpr int kSteps = kPiece / 64;        // MFMA K steps per piece
+constexpr int kRing = kWaves * 2 * kItem;  // 64 KiB
+constexpr int kRedWords = kGmvBlocks * 16 * 8;
+// Past half of the CU's 160 KiB, so the grid spreads one workgroup per CU.
+constexpr int kLds = 96 * 1024;
+static_assert(kRing + kRedWords * 4 <= kLds, "LDS plan");
+}  // namespace gmv
+
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
+                                                        int M, int64_t N, int NB, int Kpad, Epilogue ep) {
+  using namespace gmv;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[kLds];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int bb = (int)((int64_t)blockIdx.x * NB / gridDim.x);
+  const int nbl = (int)((int64_t)(blockIdx.x + 1) * NB / gridDim.x) - bb;
+  const int KP = Kpad / kPiece;
+  const int p0 = wave * KP / kWaves, p1 = (wave + 1) * KP / kWaves;
+  const int nitems = (p1 - p0) * nbl;
+  int32_t* red = reinterpret_cast<int32_t*>(smem + kRing);  // [block][row][m]
+  for (int i = threadIdx.x; i < kRedWords; i += 256) red[i] = 0;
+  __syncthreads();
+
+  int8_t* const ring = smem + wave * 2 * kItem;
+  const int8_t* const wbase = B + (int64_t)bb * 16 * Kpad;
+  const int drow = lane >> 5, dchunk = lane & 31;  // copy: two 512-byte row pieces per instruction
+  const int r = lane & 15, q = lane >> 4;          // fragment: row / column r, K quarter q
+  const int8_t* const xrow = A + (int64_t)(r < M ? r : M - 1) * Kpad + q * 16;
+  v4i xs[kSteps], xc[kSteps], acc[kGmvBlocks];
+#pragma unroll
+  for (int b = 0; b < kGmvBlocks; b++) acc[b] = v4i{0, 0, 0, 0};
+  // The activation fragments of piece p; issued with the piece's first item,
+  // so they land before its copies.
+  auto load_x = [&](int p) {
+#pragma unroll
+    for (int s = 0; s < kSteps; s++) xs[s] = *reinterpret_cast<const v4i*>(xrow + p * kPiece + s * 64);
+  };
+  // Item (p, b) into stage `stage`.
+  auto issue = [&](int p, int b, int stage) {
+    const int8_t* src = wbase + (int64_t)b * 16 * Kpad + p * kPiece;
+    int8_t* dst = ring + stage * kItem;
+#pragma unroll
+    for (int j = 0; j < kDma; j++) {
+      const int rr = 2 * j + drow;
+      dma16(src + (int64_t)rr * Kpad + ((dchunk ^ rr) << 4), dst + j * 1024);
+    }
+  };
+  if (nitems > 0) {
+    load_x(p0);
+    issue(p0, 0, 0);
+  }
+  int i = 0;
+  for (int p = p0; p < p1; p++) {
+#pragma unroll
+    for (int b = 0; b < kGmvBlocks; b++) {
+      if (b < nbl) {
+        wait_vmcnt<0>();  // item i (and, at b == 0, the piece's activations) landed
+        if (b == 0) {
+#pragma unroll
+          for (int s = 0; s < kSteps; s++) xc[s] = r < M ? xs[s] : v4i{0, 0, 0, 0};
+        }
+        if (i + 1 < nitems) {
+          if (b + 1 == nbl) {
+            load_x(p + 1);
+            issue(p + 1, 0, (i + 1) & 1);
+          } else {
+            issue(p, b + 1, (i + 1) & 1);
+          }
+        }
+        const int8_t* st = ring + (i & 1) * kItem + r * kPiece;
+#pragma unroll
+        for (int s = 0; s < kSteps; s++) {
+          const v4i wf = *reinterpret_cast<const v4i*>(st + (((4 * s + q) ^ r) << 4));
+          acc[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, xc[s], acc[b], 0, 0, 0);
+        }
+        // this stage's reads are done before a later copy refills it
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        i++;
+      }
+    }
+  }
+  // lane l holds D[4 q + e][r]: rows 4q..4q+3 of each block, column r
+  if (r < M) {
+#pragma unroll
+    for (int b = 0; b < kGmvBlocks; b++)
+      if (b < nbl) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) atomicAdd(&red[(b * 16 + 4 * q + e) * 8 + r], acc[b][e]);
+      }
+  }
+  __syncthreads();
+
+  const float cs = tensor_scale(ep.absmax_in) * ep.w_scale;
+  const int rows = nbl * 16;
+  uint32_t amax = 0;
+  for (int idx = threadIdx.x; idx < rows * M; idx += 256) {
+    const int m = idx / rows, nl = idx - m * rows;
+    const int64_t col = (int64_t)bb * 16 + nl;
+    if (col < N) {
+      const int32_t sum = red[nl * 8 + m];
+      const float prod = (float)sum * cs;
+      const float pre = prod + ep.bias[col];
+      float v;
+      switch (ep.act) {
+        case rgmath::ACT_RELU: v = act_fixed<rgmath::ACT_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SIGMOID: v = act_fixed<rgmath::ACT_SIGMOID>(pre, ep.act_param); break;
+        case rgmath::ACT_TANH: v = act_fixed<rgmath::ACT_TANH>(pre, ep.act_param); break;
+        case rgmath::ACT_GELU: v = act_fixed<rgmath::ACT_GELU>(pre, ep.act_param); break;
+        case rgmath::ACT_LEAKY_RELU: v = act_fixed<rgmath::ACT_LEAKY_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SILU: v = act_fixed<rgmath::ACT_SILU>(pre, ep.act_param); break;
+        default: v = pre; break;
+      }
+      ep.y[m * N + col] = v;
+      if (ep.acc_out) ep.acc_out[m * N + col] = sum;
+      const uint32_t key = rgmath::absmax_key(v);
+      amax = key > amax ? key : amax;
+    }
+  }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
+  }
+}
+
+bool gemv_mfma_supported(int64_t M, int64_t Npad, int64_t Kpad) {
+  // Row counts and shapes where the matrix-core form beats the dot4 form:
+  // enough row blocks for every CU and whole 512-byte K pieces, at least
+  // one per wave.
+  return M >= kGmvMinRows && M <= 8 && Kpad % gmv::kPiece == 0 && Kpad >= gmv::kWaves * gmv::kPiece &&
+         Kpad <= INT32_MAX && Npad / 16 >= 256;
+}
+
+static void launch_gemv_mfma(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
+                             const Epilogue& ep, hipStream_t s) {
+  const void* fn = reinterpret_cast<const void*>(&gemv_mfma_kernel);
+  static const int64_t cap = resident_blocks(fn);
+  const int64_t NB = Npad / 16;
+  int64_t grid = cap < NB ? cap : NB;
+  const int64_t need = (NB + kGmvBlocks - 1) / kGmvBlocks;  // at most kGmvBlocks blocks per workgroup
+  if (grid < need) grid = need;
+  RG_LAUNCH(gemv_mfma_kernel, dim3((unsigned)grid), dim3(256), 0, s, A, B, (int)M, N, (int)NB, (int)Kpad, ep);
+}
+
 // Linear with at most 16 outputs per row (the classifier heads: D's
 // 1024 -> 10, C's 256 -> 10, Q's 32 -> 3).  A 128 x 128 MFMA tile would waste
 // most of its columns, so a wave takes one row at a time instead: lane l
@@ -1419,7 +1589,10 @@ void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N
 
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad,
                  const Epilogue& ep, hipStream_t s) {
-  launch_gemv_any<kModeI8>(A, B, M, N, Npad, Kpad, ep, s);
+  if (gemv_mfma_supported(M, Npad, Kpad))
+    launch_gemv_mfma(A, B, M, N, Npad, Kpad, ep, s);
+  else
+    launch_gemv_any<kModeI8>(A, B, M, N, Npad, Kpad, ep, s);
 }
 
 void launch_gemv_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Npad, int64_t Kpad_f,

@@ -168,6 +168,13 @@ void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int
                             const Epilogue& ep, hipStream_t s);
 void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Kpad_f, const Epilogue& ep,
                             hipStream_t s);
+// INT8 GEMV for M <= 8 rows: the matrix-core form (row blocks of 16
+// weights streamed through LDS) where gemv_mfma_supported, else the dot4
+// form.  kGmvBlocks: most 16-row blocks one workgroup of the matrix-core
+// form keeps accumulators for; kGmvMinRows: fewest rows it is used for.
+constexpr int kGmvBlocks = 8;
+constexpr int kGmvMinRows = 2;
+bool gemv_mfma_supported(int64_t M, int64_t Npad, int64_t Kpad);
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
                  int64_t Kpad, const Epilogue& ep, hipStream_t s);
 

@@ -9,7 +9,11 @@ Bit for bit against the oracle, capture taps included:
 * inputs holding NaN, +-inf and the absmax at the last column;
 * K % 4 != 0 (element loads), a long K (the input larger than one
   workgroup keeps), and an input pointer that is not 16-byte aligned
-  (run_device on an offset buffer).
+  (run_device on an offset buffer);
+* the matrix-core form (M >= 2, K a multiple of 512, at least 4096 output
+  rows): 512-byte K pieces that do not split evenly over a workgroup's 4
+  waves, N not a multiple of 16, a grid of more workgroups than CUs (more
+  than 8 row blocks per CU), and a GEMV after a GEMV.
 """
 import numpy as np
 import pytest
@@ -86,3 +90,29 @@ def test_unaligned_device_input(rg, ref):
     sess.synchronize()
     assert_bitexact_f32(d_y.download((2, 256)), want, "gemv aligned input")
     sess.close()
+
+
+MFMA_CASES = [
+    # (dims, rows): 2560 = 5 K pieces over 4 waves; 4100 outputs -> 272 row
+    # blocks, the last one partly padding; 33000 -> 2064 blocks, 258
+    # workgroups of at most 8; [.., 4096, 4608] a GEMV feeding a GEMV
+    ([2560, 4100, 64], 2),
+    ([2560, 4100, 64], 5),
+    ([2560, 4100, 64], 8),
+    ([2048, 33000, 16], 3),
+    ([3072, 4096, 4608, 40], 7),
+]
+
+
+@pytest.mark.parametrize("dims,rows", MFMA_CASES, ids=[f"{c[0][1]}-M{c[1]}" for c in MFMA_CASES])
+def test_gemv_matrix_core_form(rg, ref, dims, rows):
+    layers = _mlp(rg, dims, seed=rows * 7 + dims[1], act="tanh")
+    x = rg.randn([rows, dims[0]])
+    check_against_oracle(rg, ref, layers, x, f"gemv mfma {dims} M={rows}")
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y = sess.run(x)
+    y2 = sess.run(x)
+    sess.close()
+    want = ref.RefProgram(layers).run(x)
+    assert_bitexact_f32(y, want, f"gemv mfma {dims} M={rows} (no capture)")
+    assert_bitexact_f32(y2, want, f"gemv mfma {dims} M={rows} (second run)")
