@@ -1252,6 +1252,188 @@ static void launch_gemv_any(const int8_t* A, const int8_t* B, int64_t M, int64_t
   }
 }
 
+// One-row INT8 GEMV that quantizes its own f32 input (QuantTensor::from_f32,
+// quantize.rs:18-24 at npu.rs:312, then quantize.rs:104-113), so no
+// quantize launch precedes it.  Each thread reads its share of the row into
+// registers, then each wave issues the weight loads of its first trip; while
+// they are in flight the workgroup stages the quantized row in LDS (the
+// same quantize_one rule as quant_rows_kernel),
+// with the scale from the spread slot the producer raised or, for a Linear
+// whose input has no absmax yet (SELF), from the input's absmax, which every
+// workgroup reduces itself from L2.  The weights then stream as in
+// gemv_kernel<1, 4, 4, 0> (same lanes, same per-lane sdot4 order, same
+// reduce-scatter and epilogue).  Workgroup 0 writes the i8 row and the
+// scale to the capture taps when they are given.
+constexpr int kGemvXqR = 4, kGemvXqU = 4;
+
+template <bool SELF>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void gemv_xq_kernel(const float* __restrict__ x, const int8_t* __restrict__ B,
+                                                      int64_t N, int64_t groups, int64_t K, int64_t Kpad, Epilogue ep,
+                                                      int8_t* q_out, float* scale_out, SlotClear clear) {
+  constexpr int R = kGemvXqR, U = kGemvXqU;
+  constexpr int S = pow2_at_least(R);
+  constexpr int SPREAD = 64 / S;
+  __shared__ __attribute__((aligned(16))) int8_t xl[kGemvXqMaxK];
+  __shared__ uint32_t red[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  const int64_t g0 = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t ntrip = (Kpad + 1024 * U - 1) / (1024 * U);
+  const int64_t klast = Kpad - 16;
+  auto load_w = [&](int64_t g, int64_t t, v4i (&w)[U][R]) {
+    const int8_t* wrow = B + g * R * Kpad;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int64_t k = (t * U + u) * 1024 + lane * 16;
+      const int64_t kk = k < Kpad ? k : klast;
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + r * Kpad + kk));
+    }
+  };
+  // The whole row is read into registers first (8 float4 per thread, zeros
+  // past K), then the slot partial, then the first trip's weights: vector
+  // loads complete in issue order, so the row and the slot are usable while
+  // the weights are still in flight.
+  constexpr int XB = kGemvXqMaxK / 1024;
+  const v4f* const x4 = reinterpret_cast<const v4f*>(x);
+  const int K4 = (int)(K >> 2), Kp4 = (int)(Kpad >> 2);
+  v4f v[XB];
+#pragma unroll
+  for (int j = 0; j < XB; j++) {
+    const int c = (int)threadIdx.x + 256 * j;
+    v[j] = c < K4 ? x4[c] : v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  uint32_t part = 0;
+  if constexpr (!SELF) part = tensor_absmax_part(ep.absmax_in);
+  // (issued unconditionally, clamped to the last group, so the waits below
+  // count exactly these 16 loads as the newer ones)
+  v4i w[U][R];
+  load_w(g0 < groups ? g0 : groups - 1, 0, w);
+  // The row is used only after this point, so its wait (vmcnt(16)) and the
+  // staging arithmetic stay behind the weight loads.
+#pragma unroll
+  for (int j = 0; j < XB; j++) asm volatile("" : "+v"(v[j]));
+  // A workgroup barrier without the fence of __syncthreads, whose vmcnt(0)
+  // would wait for the weights: LDS writes complete first, then s_barrier.
+  auto lds_barrier = [] {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  uint32_t m;
+  if constexpr (SELF) {
+    m = 0;
+#pragma unroll
+    for (int j = 0; j < XB; j++) {
+      const uint32_t a = max(rgmath::absmax_key(v[j][0]), rgmath::absmax_key(v[j][1]));
+      const uint32_t b = max(rgmath::absmax_key(v[j][2]), rgmath::absmax_key(v[j][3]));
+      m = max(m, max(a, b));
+    }
+    m = wave_max_u32(m);
+    if (lane == 0) red[wave] = m;
+    lds_barrier();
+    m = max(max(red[0], red[1]), max(red[2], red[3]));
+  } else {
+    m = wave_max_u32(part);
+  }
+  const float scale = rgmath::scale_from_absmax(rgmath::bitsf(m));
+  const float inv = 1.0f / scale;
+  uint32_t* const xw = reinterpret_cast<uint32_t*>(xl);
+#pragma unroll
+  for (int j = 0; j < XB; j++) {
+    const int c = (int)threadIdx.x + 256 * j;
+    if (c < Kp4) xw[c] = pack4(v[j][0], v[j][1], v[j][2], v[j][3], inv);
+  }
+  lds_barrier();
+  // (after the staging: clear_slots reads the block size from the dispatch
+  // packet with a vector load, whose wait would also wait for the weights)
+  if constexpr (SELF) clear_slots(clear);
+  if (blockIdx.x == 0) {
+    if (q_out)
+      for (int64_t i = threadIdx.x; i < Kp4; i += 256) reinterpret_cast<uint32_t*>(q_out)[i] = xw[i];
+    if (scale_out && threadIdx.x == 0) *scale_out = scale;
+  }
+
+  const float cs = scale * ep.w_scale;
+  const int sidx = lane / SPREAD;
+  const int orr = sidx % R;
+  const bool owner = (lane % SPREAD) == 0 && sidx < R;
+  uint32_t amax = 0;
+  for (int64_t g = g0; g < groups; g += waves) {
+    const int64_t col = g * R + orr;
+    const float bias_v = ep.bias[col < N ? col : N - 1];
+    int32_t acc[S];
+#pragma unroll
+    for (int i = 0; i < S; i++) acc[i] = 0;
+    for (int64_t t = 0; t < ntrip; t++) {
+      // the first trip of the first group was issued before the staging
+      if (g != g0 || t != 0) load_w(g, t, w);
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int64_t k = (t * U + u) * 1024 + lane * 16;
+        const bool ok = k < Kpad;
+        const v4i xr = *reinterpret_cast<const v4i*>(xl + (ok ? k : klast));
+        const v4i xv = ok ? xr : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          int32_t a = acc[r];
+          a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
+          a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
+          a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
+          a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+          acc[r] = a;
+        }
+      }
+    }
+    const int32_t mine = wave_reduce_scatter<S, false>(acc, lane);
+    const float prod = (float)mine * cs;
+    const float pre = prod + bias_v;
+    if (owner && col < N) {
+      float v;
+      switch (ep.act) {
+        case rgmath::ACT_RELU: v = act_fixed<rgmath::ACT_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SIGMOID: v = act_fixed<rgmath::ACT_SIGMOID>(pre, ep.act_param); break;
+        case rgmath::ACT_TANH: v = act_fixed<rgmath::ACT_TANH>(pre, ep.act_param); break;
+        case rgmath::ACT_GELU: v = act_fixed<rgmath::ACT_GELU>(pre, ep.act_param); break;
+        case rgmath::ACT_LEAKY_RELU: v = act_fixed<rgmath::ACT_LEAKY_RELU>(pre, ep.act_param); break;
+        case rgmath::ACT_SILU: v = act_fixed<rgmath::ACT_SILU>(pre, ep.act_param); break;
+        default: v = pre; break;
+      }
+      ep.y[col] = v;
+      if (ep.acc_out) ep.acc_out[col] = mine;
+      const uint32_t key = rgmath::absmax_key(v);
+      amax = key > amax ? key : amax;
+    }
+  }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
+  }
+}
+
+bool gemv_xq_supported(int64_t M, int64_t K, int64_t Kpad, const void* x) {
+  return M == 1 && K % 4 == 0 && Kpad <= kGemvXqMaxK && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+
+void launch_gemv_xq(const float* x, const int8_t* B, int64_t N, int64_t Npad, int64_t K, int64_t Kpad,
+                    const Epilogue& ep, bool self_absmax, int8_t* q_out, float* scale_out, const SlotClear& clear,
+                    hipStream_t s) {
+  const int64_t groups = Npad / kGemvXqR;
+  const int64_t want = (groups + 3) / 4;
+  if (self_absmax) {
+    static const int64_t cap = resident_blocks(reinterpret_cast<const void*>(&gemv_xq_kernel<true>));
+    RG_LAUNCH(gemv_xq_kernel<true>, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, x, B, N, groups, K,
+              Kpad, ep, q_out, scale_out, clear);
+  } else {
+    static const int64_t cap = resident_blocks(reinterpret_cast<const void*>(&gemv_xq_kernel<false>));
+    RG_LAUNCH(gemv_xq_kernel<false>, dim3((unsigned)(want < cap ? want : cap)), dim3(256), 0, s, x, B, N, groups,
+              K, Kpad, ep, q_out, scale_out, clear);
+  }
+}
+
 // INT8 GEMV on the matrix cores for a few rows (quantize.rs:104-113 with
 // M <= 8): y[m][n] = act(fl(float(sum_k x[m][k] w[n][k]) * cs) + b[n]).
 //

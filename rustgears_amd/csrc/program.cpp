@@ -1056,7 +1056,10 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         const bool narrow_xq = !pl.gemv && op.out_f <= kNarrowMaxN && !pl.explicit_absmax && !pl.q_ready &&
                                pl.rows > 0 && gemm_narrow_xq_supported(op.in_f, op.Kpad) &&
                                (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-        if (narrow_xq) {
+        // A one-row GEMV quantizes its input itself, with the producer's
+        // absmax or, when its input has none yet, the input's own.
+        const bool gemv_xq = pl.gemv && !pl.q_ready && gemv_xq_supported(pl.rows, op.in_f, op.Kpad, in);
+        if (narrow_xq || gemv_xq) {
           // nothing before the GEMM
         } else if (pl.iq_sync_base >= 0) {
           launch_input_quant(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base,
@@ -1091,6 +1094,11 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             rq.keep_f32 = cap ? 1 : 0;
             rq.spin_limit = plan.spin_limit;
             launch_gemm_requant(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, rq, s);
+          } else if (gemv_xq) {
+            launch_gemv_xq(in, op.d_w.as<int8_t>(), op.out_f, op.Npad, op.in_f, op.Kpad, ep, pl.explicit_absmax,
+                           cap ? qa : nullptr, cap ? scales + pl.scale_base : nullptr,
+                           pl.explicit_absmax ? clear : SlotClear{}, s);
+            if (pl.explicit_absmax) first_launched();
           } else if (pl.gemv) {
             launch_gemv(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
           } else if (narrow_xq) {

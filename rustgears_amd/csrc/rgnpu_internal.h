@@ -175,6 +175,15 @@ void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N
 constexpr int kGmvBlocks = 8;
 constexpr int kGmvMinRows = 2;
 bool gemv_mfma_supported(int64_t M, int64_t Npad, int64_t Kpad);
+// One-row INT8 GEMV reading its f32 input x [K] and quantizing it itself:
+// with the scale of the spread slot ep.absmax_in (a producer raised it) or,
+// with self_absmax, from x's own absmax (then it also takes the run's slot
+// clearing).  q_out [Kpad] / scale_out (nullable): capture taps.
+constexpr int kGemvXqMaxK = 8192;  // the row a workgroup holds in registers (8 float4 per thread)
+bool gemv_xq_supported(int64_t M, int64_t K, int64_t Kpad, const void* x);
+void launch_gemv_xq(const float* x, const int8_t* B, int64_t N, int64_t Npad, int64_t K, int64_t Kpad,
+                    const Epilogue& ep, bool self_absmax, int8_t* q_out, float* scale_out, const SlotClear& clear,
+                    hipStream_t s);
 void launch_gemv(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t Npad,
                  int64_t Kpad, const Epilogue& ep, hipStream_t s);
 

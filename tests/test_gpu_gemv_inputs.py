@@ -13,7 +13,11 @@ Bit for bit against the oracle, capture taps included:
 * the matrix-core form (M >= 2, K a multiple of 512, at least 4096 output
   rows): 512-byte K pieces that do not split evenly over a workgroup's 4
   waves, N not a multiple of 16, a grid of more workgroups than CUs (more
-  than 8 row blocks per CU), and a GEMV after a GEMV.
+  than 8 row blocks per CU), and a GEMV after a GEMV;
+* the one-row form that quantizes its own f32 input: with the input's own
+  absmax (the run's first Linear) and with the producer's, K at the largest
+  row it stages (8192) and just past it, K % 4 != 0 and an unaligned input
+  (both take the separate quantize pass).
 """
 import numpy as np
 import pytest
@@ -116,3 +120,53 @@ def test_gemv_matrix_core_form(rg, ref, dims, rows):
     want = ref.RefProgram(layers).run(x)
     assert_bitexact_f32(y, want, f"gemv mfma {dims} M={rows} (no capture)")
     assert_bitexact_f32(y2, want, f"gemv mfma {dims} M={rows} (second run)")
+
+
+XQ_CASES = [
+    # (dims, what)
+    ([8192, 4096, 8192, 24], "largest staged row, twice"),
+    ([8196, 1024, 512], "row past the staged limit"),
+    ([1022, 2048, 4100, 64], "K % 4 != 0 first, then staged"),
+    ([4000, 28672, 8192], "staged, then a row past the limit"),
+]
+
+
+@pytest.mark.parametrize("dims,what", XQ_CASES, ids=[c[1] for c in XQ_CASES])
+def test_gemv_one_row_quantizing_its_input(rg, ref, dims, what):
+    layers = _mlp(rg, dims, seed=dims[0] + len(dims), act="gelu")
+    x = rg.randn([1, dims[0]])
+    x[0, dims[0] - 1] = 17.75  # the absmax at the last column
+    check_against_oracle(rg, ref, layers, x, f"gemv xq {what}")
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y = sess.run(x)
+    y2 = sess.run(x)
+    sess.close()
+    want = ref.RefProgram(layers).run(x)
+    assert_bitexact_f32(y, want, f"gemv xq {what} (no capture)")
+    assert_bitexact_f32(y2, want, f"gemv xq {what} (second run)")
+
+
+def test_gemv_one_row_unaligned_input(rg, ref):
+    from rustgears_amd.inference import DeviceBuffer
+    layers = _mlp(rg, [2048, 4096, 300], seed=11)
+    x = rg.randn([1, 2048])
+    want = ref.RefProgram(layers).run(x)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    buf = DeviceBuffer(x.nbytes + 16)
+    padded = np.zeros(x.size + 4, np.float32)
+    padded[1:1 + x.size] = x.reshape(-1)
+    buf.upload(padded)
+
+    class Offset:  # the same allocation, 4 bytes in
+        ptr = buf.ptr + 4
+        nbytes = x.nbytes
+
+    d_y = DeviceBuffer(300 * 4)
+    assert sess.run_device(Offset, x.shape, d_y) == (1, 300)
+    sess.synchronize()
+    assert_bitexact_f32(d_y.download((1, 300)), want, "gemv one row, unaligned input")
+    d_x = DeviceBuffer.from_array(x)
+    sess.run_device(d_x, x.shape, d_y)
+    sess.synchronize()
+    assert_bitexact_f32(d_y.download((1, 300)), want, "gemv one row, aligned input")
+    sess.close()
