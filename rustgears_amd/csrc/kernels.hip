@@ -1494,9 +1494,14 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const int8_t* __restrict
   for (int b = 0; b < kGmvBlocks; b++) acc[b] = v4i{0, 0, 0, 0};
   // The activation fragments of piece p; issued with the piece's first item,
   // so they land before its copies.
-  auto load_x = [&](int p) {
+  // (only lanes whose batch row exists load; the others use zeros)
 #pragma unroll
-    for (int s = 0; s < kSteps; s++) xs[s] = *reinterpret_cast<const v4i*>(xrow + p * kPiece + s * 64);
+  for (int s = 0; s < kSteps; s++) xs[s] = v4i{0, 0, 0, 0};
+  auto load_x = [&](int p) {
+    if (r < M) {
+#pragma unroll
+      for (int s = 0; s < kSteps; s++) xs[s] = *reinterpret_cast<const v4i*>(xrow + p * kPiece + s * 64);
+    }
   };
   // Item (p, b) into stage `stage`.
   auto issue = [&](int p, int b, int stage) {
