@@ -421,6 +421,38 @@ RG_HD float gelu(float x) {
   return h * one_t;
 }
 
+// Certified GELU for the INT8 requantization (a GELU output that only feeds
+// the next Linear's QuantTensor::from_f32, quantize.rs:18-24).  Only the
+// tensor's absmax and each value's quantized integer leave such a layer, and
+// both can be had exactly without evaluating the exact GELU on every value:
+//  * absmax: on [0, +inf] the f32 GELU never decreases, and over every
+//    negative input |gelu(x)| <= kGeluNegAbsMax (both checked exhaustively
+//    on the host, tests/support/gelu_shape_check.cpp).  So over a set of
+//    pre-activations whose largest value xmax has gelu(xmax) >= that bound,
+//    the absmax of the outputs is gelu(xmax).
+//  * quantization: gelu_approx(x) is within kGeluApproxRel * |x| +
+//    kGeluApproxAbs of gelu(x) for every finite x (checked on the device for
+//    all 2^32 inputs, tests/support/devmath_gpu_check.hip).  Rounding
+//    fl(v * inv) half away from zero is monotonic in v, so when the whole
+//    interval around gelu_approx(x) rounds to one integer, that integer is
+//    the exact value's; otherwise the exact GELU is evaluated.
+constexpr float kGeluNegAbsMax = 0x1.5c3e58p-3f;  // |gelu(-0x1.8138e0p-1)|, the largest over x < 0
+constexpr float kGeluApproxRel = 0x1p-21f;        // bound on |gelu_approx(x) - gelu(x)| / |x|
+constexpr float kGeluApproxAbs = 0x1p-126f;       // plus this absolute term (subnormal results)
+
+#if defined(__HIPCC__)
+// x * sigmoid(2u) = 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3)
+// written as u = x (c1 + c3 x^2), exp(-2u) = 2^(x (k1 + k3 x^2)), by the
+// hardware exp2 and reciprocal.  Device only: the bound is a property of
+// those instructions.
+__device__ __forceinline__ float gelu_approx(float x) {
+  const float x2 = x * x;
+  const float p = __builtin_fmaf(-0.10294324f, x2, -2.3022084f);  // -2 log2(e) c1 (0.044715, 1), c1 = 0.7978846
+  const float e = __builtin_amdgcn_exp2f(x * p);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
+#endif
+
 RG_HD float act_apply(int act, float p, float x) {
   switch (act) {
     case ACT_RELU: return relu(x);

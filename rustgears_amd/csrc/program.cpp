@@ -165,6 +165,7 @@ struct Plan {
   DevBuf f32[2], q, slots, scales, masks, host_in, host_out;
   DevBuf q_alt;  // second i8 operand buffer: a fused producer writes the one its GEMM does not read
   int spin_limit = 0;  // requant barrier polls before a workgroup defers (RGNPU_REQUANT_SPIN_LIMIT)
+  int gelu_cert = 1;   // GELU requantization (RGNPU_GELU_CERT): 1 certified, 0 exact; 2, 3 test modes (requant.hip)
   DevBuf ylo;  // FP16 conv: GEMM output [n*L, O] before the NCHW transpose
   DevBuf ws;  // split-K partial sums
   int64_t ws_bytes = 0;
@@ -806,6 +807,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   }
   if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
   else plan->spin_limit = 100000;  // ~20 ms
+  if (const char* e = getenv("RGNPU_GELU_CERT")) plan->gelu_cert = std::min(3, std::max(0, atoi(e)));
   plan->n_slots = slots;
   // The first computing op quantizes the input itself (its absmax is the
   // run's first kernel) unless the input is empty.
@@ -1093,6 +1095,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             rq.scale_out = scales + cpl.scale_base;
             rq.keep_f32 = cap ? 1 : 0;
             rq.spin_limit = plan.spin_limit;
+            rq.gelu_cert = plan.gelu_cert;
             launch_gemm_requant(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, rq, s);
           } else if (gemv_xq) {
             launch_gemv_xq(in, op.d_w.as<int8_t>(), op.out_f, op.Npad, op.in_f, op.Kpad, ep, pl.explicit_absmax,

@@ -284,20 +284,305 @@ __device__ __forceinline__ void quantize_stored_flat(const float* y, int8_t* q, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Certified GELU requantization (GELU producer, no capture).  The epilogue
+// keeps and stores the pre-activations x = fl(fl(acc * cs) + b); a lane's
+// exact absmax is gelu(xmax) over its outputs (rgmath::kGeluNegAbsMax and the
+// monotonicity of the f32 GELU on [0, +inf]), with an exact walk over its
+// outputs when gelu(xmax) falls below that bound.  After the barrier each
+// value is quantized from gelu_approx(x): t = fl(g * inv) and q = round(t)
+// stand when |t - q| + m < 1/2, where m = fl(mc |x|) + m0 covers
+// (kGeluApproxRel |x| + kGeluApproxAbs) inv plus the roundings of t (|t| is
+// at most about |x| inv, since |gelu(x)| <= |x|) and of the test itself.
+// The values that miss the test (a few per 10^5; NaN and infinite x always
+// miss it: their m is not finite) go to a per-wave queue in LDS and get the
+// exact GELU once the walk is done, one queued value per lane; a queue that
+// overflows sends its wave through every value again.
+// ---------------------------------------------------------------------------
+struct CertConst {
+  float mc, m0;  // m = mc |x| + m0, in quantization steps
+};
+
+// Mode 1: the certified test.  Mode 2: every value misses it (each wave's
+// queue overflows: the full re-walk).  Mode 3: m0 raised by 1/256, so a few
+// values in a thousand miss it and go through the queue.
+__device__ __forceinline__ CertConst cert_const(float inv, int mode) {
+  CertConst c;
+  c.mc = ((rgmath::kGeluApproxRel + 0x1p-23f) * 1.0001f) * inv;
+  c.m0 = (rgmath::kGeluApproxAbs * 1.0001f) * inv + 0x1p-24f;
+  if (mode == 2) c.m0 = __builtin_inff();
+  if (mode == 3) c.m0 = c.m0 + 0x1p-8f;
+  return c;
+}
+
+// The certified quantization of one pre-activation: the quantized integer,
+// and in ok whether it is certain.
+__device__ __forceinline__ int32_t cert_q(float x, float inv, const CertConst& c, bool& ok) {
+  const float t = rgmath::gelu_approx(x) * inv;
+  const int32_t q = rgmath::quantize_rz_bounded(t);
+  const float r = __builtin_fabsf(t - (float)q);
+  const float m = c.mc * __builtin_fabsf(x) + c.m0;
+  ok = r + m < 0.5f;
+  return q;
+}
+
+// The exact quantized integer (the clamp cannot act: |gelu(x)| <= absmax).
+__device__ __forceinline__ int32_t exact_q(float x, float inv) {
+  return rgmath::quantize_rz_bounded(rgmath::gelu_fast(x) * inv);
+}
+
+// Per-wave queue of uncertain values in LDS: x bits, and the byte offset of
+// its q byte from the walk's buffer base, in two arrays.  n counts every
+// value pushed (it is wave-uniform) and may exceed the capacity.
+constexpr int kCertQueue = 512;      // entries per wave (4 KiB)
+constexpr int kCertQueueBase = 8192; // bytes from the LDS array's start (the finisher's list comes first)
+struct CertQueue {
+  uint32_t* x;
+  uint32_t* off;
+  uint32_t n;
+};
+
+__device__ __forceinline__ CertQueue cert_queue(int8_t* smem, int wave) {
+  uint32_t* const base = reinterpret_cast<uint32_t*>(smem + kCertQueueBase) + wave * 2 * kCertQueue;
+  return CertQueue{base, base + kCertQueue, 0u};
+}
+
+__device__ __forceinline__ void cert_push(CertQueue& qu, bool need, float x, uint32_t off) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
+  if (m == 0) return;
+  if (need) {
+    const uint32_t pos =
+        qu.n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (pos < (uint32_t)kCertQueue) {
+      qu.x[pos] = __float_as_uint(x);
+      qu.off[pos] = off;
+    }
+  }
+  qu.n += (uint32_t)__builtin_popcountll(m);
+}
+
+// Four certified bytes of one row (little-endian by column); the uncertain
+// ones among the valid values are queued (off: the first byte's offset).
+__device__ __forceinline__ uint32_t cert_q8x4(v4f v, float inv, const CertConst& c, bool valid, uint32_t off,
+                                              CertQueue& qu) {
+  bool o0, o1, o2, o3;
+  const uint32_t b0 = (uint32_t)cert_q(v[0], inv, c, o0), b1 = (uint32_t)cert_q(v[1], inv, c, o1);
+  const uint32_t b2 = (uint32_t)cert_q(v[2], inv, c, o2), b3 = (uint32_t)cert_q(v[3], inv, c, o3);
+  if (__builtin_amdgcn_ballot_w64(valid && !(o0 && o1 && o2 && o3))) {
+    cert_push(qu, valid && !o0, v[0], off);
+    cert_push(qu, valid && !o1, v[1], off + 1u);
+    cert_push(qu, valid && !o2, v[2], off + 2u);
+    cert_push(qu, valid && !o3, v[3], off + 3u);
+  }
+  const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Rewrites the queued bytes with the exact GELU, one entry per lane.  The
+// word stores of the walk have completed first (vmcnt(0)), so these byte
+// stores, from any lane, land after them.  Returns false when the queue
+// overflowed (nothing is rewritten then).
+__device__ __forceinline__ bool cert_drain(const CertQueue& qu, __amdgpu_buffer_rsrc_t rq, float inv, int lane) {
+  if (qu.n == 0) return true;
+  if (qu.n > (uint32_t)kCertQueue) return false;
+  wait_vmcnt<0>();
+  for (uint32_t j = (uint32_t)lane; j < qu.n; j += 64)
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)exact_q(__uint_as_float(qu.x[j]), inv), rq, (int)qu.off[j], 0, 0);
+  return true;
+}
+
+// The uncertain bytes of 4 values, rewritten with the exact GELU (the
+// overflow path: a byte store after the word store of the same thread).
+__device__ __forceinline__ void cert_fix4(__amdgpu_buffer_rsrc_t rq, v4f v, float inv, const CertConst& c, uint32_t qoff,
+                                          uint32_t soff) {
+#pragma unroll 1
+  for (int e = 0; e < 4; e++) {
+    bool ok;
+    (void)cert_q(v[e], inv, c, ok);
+    if (!ok)
+      __builtin_amdgcn_raw_buffer_store_b8((uint8_t)exact_q(v[e], inv), rq, (int)(qoff + (uint32_t)e), (int)soff, 0);
+  }
+}
+
+// The epilogue of the certified path: x = fl(fl(acc * cs) + b) in acc
+// (f32 bits) and, when `store`, in y; returns the exact max |gelu(x)| over
+// the lane's outputs.
+template <int FM>
+__device__ __forceinline__ float cert_epilogue(int8_t* smem, v4i (&acc)[FM][4], int32_t wrow0, int32_t wcol0, int32_t N,
+                                               const LaneSpan& sp, float cs, const float4 b4, const Epilogue& ep,
+                                               bool store, float thr, int wave, int lane) {
+  int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
+  const int sub = lane >> 4, c4 = (lane & 15) * 4;
+  const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + (int64_t)wrow0 * N + wcol0);
+  const uint32_t voff = (uint32_t)((sub * N + c4) * 4);
+  const uint32_t row_bytes = (uint32_t)N * 4u;
+  float xmax = 0.0f;  // a phantom 0 output: gelu(0) = 0 is no larger than the absmax
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int rr = p * 4 + sub, ro = i * 16 + p * 4;
+      const v4i a = *reinterpret_cast<const v4i*>(slab + rr * big::SLAB_LD + c4);
+      v4f v;
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[c] = epi_value<rgmath::ACT_NONE>(a[c], cs, bb[c], 0.0f);
+      const bool ok = ro < sp.rows_left && sp.cols_ok;
+      const float m4 = __builtin_fmaxf(__builtin_fmaxf(v[0], v[1]), __builtin_fmaxf(v[2], v[3]));
+      xmax = __builtin_fmaxf(xmax, ok ? m4 : 0.0f);
+      if (store)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), ry, (int)(ok ? voff : kDropOffset),
+                                               (int)((uint32_t)ro * row_bytes), 0);
+      acc[i][p] = __builtin_bit_cast(v4i, v);
+    }
+  }
+  const float gx = rgmath::gelu_fast(xmax);
+  if (gx >= thr) return gx;
+  // Rare: the lane's outputs are all small or not finite.  Walk them exactly,
+  // from y (stored here first when this is the kept tile).
+  float amax = 0.0f;
+  if (!store) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int ro = i * 16 + p * 4;
+        const bool ok = ro < sp.rows_left && sp.cols_ok;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, acc[i][p]), ry, (int)(ok ? voff : kDropOffset),
+                                               (int)((uint32_t)ro * row_bytes), 0);
+      }
+  }
+#pragma unroll 1
+  for (int k = 0; k < FM * 4; k++) {
+    const int ro = (k >> 2) * 16 + (k & 3) * 4;
+    if (!(ro < sp.rows_left && sp.cols_ok)) continue;
+    const v4f v = __builtin_bit_cast(
+        v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)voff, (int)((uint32_t)ro * row_bytes), 0));
+#pragma unroll
+    for (int c = 0; c < 4; c++) amax = __builtin_fmaxf(amax, __builtin_fabsf(rgmath::gelu_fast(v[c])));
+  }
+  return amax;
+}
+
+// quantize_kept for the certified path: acc holds the pre-activations.
+template <int FM>
+__device__ __forceinline__ void cert_quantize_kept(const v4i (&acc)[FM][4], float* y, int8_t* q, int32_t ldq,
+                                                   int32_t wrow0, int32_t wcol0, int32_t N, const LaneSpan& sp,
+                                                   float inv, const CertConst& c, CertQueue qu, int lane) {
+  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)wrow0 * ldq + wcol0);
+  const uint32_t qoff = (uint32_t)((lane >> 4) * ldq + 4 * (lane & 15));
+  const bool q_ok = wcol0 + 4 * (lane & 15) < ldq;
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int ro = i * 16 + p * 4;
+      const bool row_ok = ro < sp.rows_left;
+      const uint32_t soff = (uint32_t)ro * (uint32_t)ldq;
+      const uint32_t w =
+          cert_q8x4(__builtin_bit_cast(v4f, acc[i][p]), inv, c, row_ok && sp.cols_ok && q_ok, qoff + soff, qu);
+      __builtin_amdgcn_raw_buffer_store_b32(row_ok && sp.cols_ok ? w : 0u, rq, (int)(q_ok ? qoff : kDropOffset),
+                                            (int)soff, 0);
+    }
+  if (cert_drain(qu, rq, inv, lane)) return;
+  // Overflow: store the pre-activations (outputs only), then rewrite every
+  // uncertain byte from them.
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)wrow0 * N + wcol0);
+  const uint32_t voff = (uint32_t)(((lane >> 4) * N + 4 * (lane & 15)) * 4);
+  const bool lane_ok = sp.cols_ok && q_ok;
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int ro = i * 16 + p * 4;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, acc[i][p]), ry,
+                                             (int)(ro < sp.rows_left && lane_ok ? voff : kDropOffset),
+                                             (int)((uint32_t)ro * (uint32_t)N * 4u), 0);
+    }
+  if (!lane_ok) return;
+#pragma unroll 1
+  for (int k = 0; k < FM * 4; k++) {
+    const int ro = (k >> 2) * 16 + (k & 3) * 4;
+    if (!(ro < sp.rows_left)) continue;
+    const v4f v = __builtin_bit_cast(
+        v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)voff, (int)((uint32_t)ro * (uint32_t)N * 4u), 0));
+    cert_fix4(rq, v, inv, c, qoff, (uint32_t)ro * (uint32_t)ldq);
+  }
+}
+
+// quantize_stored_flat for the certified path: y holds the pre-activations.
+template <int BM, int BN, int NTHREADS>
+__device__ __forceinline__ void cert_quantize_stored_flat(const float* y, int8_t* q, int32_t ldq, int32_t m0,
+                                                          int32_t n0, int32_t M, int32_t N, float inv,
+                                                          const CertConst& cc, CertQueue qu, int tid) {
+  constexpr int C4 = BN / 4, PER = BM * C4 / NTHREADS, BATCH = PER < 16 ? PER : 16;
+  static_assert(PER * NTHREADS == BM * C4 && PER % BATCH == 0 && NTHREADS % C4 == 0, "tile walk");
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)m0 * N + n0);
+  const __amdgpu_buffer_rsrc_t rq = bounded_rsrc(q + (int64_t)m0 * ldq + n0);
+  const int c4 = tid % C4, rt = tid / C4;
+  constexpr int RSTEP = NTHREADS / C4;
+  const bool col_ok = n0 + 4 * c4 < N, q_ok = n0 + 4 * c4 < ldq;
+  const int32_t rows_left = M - m0 - rt;
+  const uint32_t voff = (uint32_t)((rt * N + 4 * c4) * 4), qoff = (uint32_t)(rt * ldq + 4 * c4);
+#pragma unroll
+  for (int k0 = 0; k0 < PER; k0 += BATCH) {
+    v4f v[BATCH];
+#pragma unroll
+    for (int k = 0; k < BATCH; k++) {
+      const int rr = (k0 + k) * RSTEP;
+      const bool ok = rr < rows_left && col_ok;
+      v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 0));
+    }
+#pragma unroll
+    for (int k = 0; k < BATCH; k++) {
+      const int rr = (k0 + k) * RSTEP;
+      const bool row_ok = rr < rows_left;
+      const uint32_t soff = (uint32_t)rr * (uint32_t)ldq;
+      const uint32_t w = cert_q8x4(v[k], inv, cc, row_ok && col_ok && q_ok, qoff + soff, qu);
+      __builtin_amdgcn_raw_buffer_store_b32(row_ok && col_ok ? w : 0u, rq, (int)(q_ok ? qoff : kDropOffset),
+                                            (int)soff, 0);
+    }
+  }
+  if (cert_drain(qu, rq, inv, tid & 63)) return;
+  // Overflow: rewrite every uncertain byte from the stored pre-activations.
+  if (!(col_ok && q_ok)) return;
+#pragma unroll 1
+  for (int k = 0; k < PER; k++) {
+    const int rr = k * RSTEP;
+    if (!(rr < rows_left)) continue;
+    const v4f v = __builtin_bit_cast(
+        v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)voff, (int)((uint32_t)rr * (uint32_t)N * 4u), 0));
+    cert_fix4(rq, v, inv, cc, qoff, (uint32_t)rr * (uint32_t)ldq);
+  }
+}
+
 // Per-launch constants of the fused kernel, 32-bit where the plan bounds
 // them (the fused path requires N % 4 == 0 and 128 N * 4 < 2^31).
 struct RequantShape {
   int32_t M, N, ldq, nk, tiles_m, tiles_n;
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP>
+// CERT: the certified GELU path (ACT == GELU, no capture): the f32 tiles
+// stored for the quantization hold pre-activations, and the GELU is
+// evaluated exactly only where the certified bound cannot decide.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP, bool CERT>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kernel(
     const int8_t* __restrict__ A, const int8_t* __restrict__ B, RequantShape sh, Epilogue ep, Requant rq) {
   using namespace big;
+  static_assert(!CERT || (ACT == rgmath::ACT_GELU && !CAP), "certified path: GELU without capture");
+  const float cert_thr = rq.gelu_cert == 2 ? __builtin_inff() : rgmath::kGeluNegAbsMax;
   constexpr int NW = WAVES_M * WAVES_N;
   static_assert(BM == 16 * FM * WAVES_M && BN == 64 * WAVES_N, "wave tile is (16 FM) x 64");
   constexpr int ST = (BM + BN) * BK;
   static_assert(NW * SLAB <= STAGES * ST, "epilogue slabs reuse the ring");
+  static_assert(!CERT || kCertQueueBase + 8 * kCertQueue * NW <= STAGES * ST, "certified queues fit in the ring");
+  static_assert(rqk::kMaxGrid * 4 <= kCertQueueBase, "the finisher's list precedes the queues");
   // One LDS array only, the few words of block state at its end: with a
   // second __shared__ variable the compiler no longer tells the ring's DMA
   // writes (global_load_lds) apart from the K loop's LDS reads and waits for
@@ -332,8 +617,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
                                                              wm, wn, lane, acc);
     if (it == 0) cs = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(absmax_part))) * ep.w_scale;
     const LaneSpan sp = lane_span(m0 + wrow, n0 + wcolw, M, N, lane);
-    const float t = requant_epilogue<ACT, FM, CAP>(smem, acc, m0 + wrow, n0 + wcolw, N, sp, cs, b4, ep,
-                                                   it + 1 < ntile || rq.keep_f32, wave, lane);
+    float t;
+    if constexpr (CERT)
+      t = cert_epilogue<FM>(smem, acc, m0 + wrow, n0 + wcolw, N, sp, cs, b4, ep, it + 1 < ntile, cert_thr, wave,
+                            lane);
+    else
+      t = requant_epilogue<ACT, FM, CAP>(smem, acc, m0 + wrow, n0 + wcolw, N, sp, cs, b4, ep,
+                                         it + 1 < ntile || rq.keep_f32, wave, lane);
     amax = __builtin_fmaxf(amax, t);
   }
 
@@ -379,13 +669,22 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
       __hip_atomic_load(ep.absmax_out + lane * kSpreadStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const float scale = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
   const float inv = 1.0f / scale;
+  const CertConst cc = cert_const(inv, rq.gelu_cert);
   // the last tile from registers, then the earlier tiles from their stored outputs
-  quantize_kept<FM>(acc, rq.q, sh.ldq, m0 + wrow, n0 + wcolw, sp_last, inv, lane);
+  if constexpr (CERT)
+    cert_quantize_kept<FM>(acc, ep.y, rq.q, sh.ldq, m0 + wrow, n0 + wcolw, N, sp_last, inv, cc,
+                           cert_queue(smem, wave), lane);
+  else
+    quantize_kept<FM>(acc, rq.q, sh.ldq, m0 + wrow, n0 + wcolw, sp_last, inv, lane);
   __builtin_amdgcn_sched_barrier(0);
   for (int it = 0; it + 1 < ntile; it++) {
     int tm, tn;
     tile_coords(b + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
-    quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
+    if constexpr (CERT)
+      cert_quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, cc,
+                                                 cert_queue(smem, wave), tid);
+    else
+      quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
   }
   if (flag != 2) return;
 
@@ -400,24 +699,28 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
     for (int it = 0; it < wt; it++) {
       int tm, tn;
       tile_coords(w + it * G, sh.tiles_m, sh.tiles_n, tm, tn);
-      quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
+      if constexpr (CERT)
+        cert_quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, cc,
+                                                   cert_queue(smem, wave), tid);
+      else
+        quantize_stored_flat<BM, BN, NW * 64>(ep.y, rq.q, sh.ldq, tm * BM, tn * BN, M, N, inv, tid);
     }
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int OCC, int FM, int ACT, bool CAP, bool CERT = false>
 static void launch_requant_act(const int8_t* A, const int8_t* B, const RequantShape& sh, int64_t Mpad, int64_t Npad,
                                int64_t Kpad, const Epilogue& ep, const Requant& rq, hipStream_t s) {
   constexpr int threads = WAVES_M * WAVES_N * 64;
   const void* fn =
-      reinterpret_cast<const void*>(&gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP>);
+      reinterpret_cast<const void*>(&gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP, CERT>);
   static const int64_t cap = resident_blocks(fn, threads);
   const int64_t T = (int64_t)sh.tiles_m * sh.tiles_n;
   int64_t G = T < cap ? T : cap;
   if (G > rqk::kMaxGrid) G = rqk::kMaxGrid;
   if (rqk::kGoBase + G * rqk::kLine > requant_sync_words(Mpad, Npad, Kpad))
     throw std::logic_error("requant: more workgroups than sync words");
-  RG_LAUNCH((gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP>), dim3((unsigned)G),
+  RG_LAUNCH((gemm_requant_kernel<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, ACT, CAP, CERT>), dim3((unsigned)G),
             dim3(threads), 0, s, A, B, sh, ep, rq);
 }
 
@@ -430,7 +733,16 @@ static void launch_requant_shape(const int8_t* A, const int8_t* B, const Requant
     case rgmath::ACT_RELU: RG_RQ(rgmath::ACT_RELU); break;
     case rgmath::ACT_SIGMOID: RG_RQ(rgmath::ACT_SIGMOID); break;
     case rgmath::ACT_TANH: RG_RQ(rgmath::ACT_TANH); break;
-    case rgmath::ACT_GELU: RG_RQ(rgmath::ACT_GELU); break;
+    case rgmath::ACT_GELU:
+      if constexpr (!CAP) {
+        if (rq.gelu_cert) {
+          launch_requant_act<BM, BN, WAVES_M, WAVES_N, STAGES, OCC, FM, rgmath::ACT_GELU, false, true>(
+              A, B, sh, Mpad, Npad, Kpad, ep, rq, s);
+          break;
+        }
+      }
+      RG_RQ(rgmath::ACT_GELU);
+      break;
     case rgmath::ACT_LEAKY_RELU: RG_RQ(rgmath::ACT_LEAKY_RELU); break;
     case rgmath::ACT_SILU: RG_RQ(rgmath::ACT_SILU); break;
     default: RG_RQ(rgmath::ACT_NONE); break;

@@ -61,6 +61,7 @@ struct Requant {
   float* scale_out = nullptr; // nullable: the scale used (capture tap)
   int keep_f32 = 0;           // also store every f32 output (capture)
   int spin_limit = 0;         // barrier polls (~0.2 us each) before a workgroup defers its quantization
+  int gelu_cert = 1;          // GELU without capture: 1 certified path, 0 exact; 2 and 3 test modes (cert_const)
 };
 constexpr int64_t kRequantStateBase = 320;
 

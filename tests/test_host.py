@@ -210,6 +210,29 @@ def test_fast_quantizer_matches_quantize_rule(tmp_path):
     assert int(out[0]) == 0x7f800000 and int(out[1]) == 0, f"bound fails at absmax 0x{out[2]}"
 
 
+def test_gelu_shape_for_certified_requantization(tmp_path):
+    """The two properties of the exact f32 GELU (rgmath::gelu, equal to the
+    reference's glibc form on every input) that let the INT8 GELU
+    requantization take the tensor absmax from the largest pre-activation:
+    it never decreases on [0, +inf], and |gelu(x)| <= kGeluNegAbsMax for every
+    negative x, with equality at x = -0x1.8138e0p-1.  Every 16th block of 2^16
+    consecutive bit patterns (all of them with RG_EXHAUSTIVE=1)."""
+    exe = tmp_path / "gshape"
+    src = os.path.join(ROOT, "tests", "support", "gelu_shape_check.cpp")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-pthread", "-o", str(exe), src, "-lm"],
+                   check=True)
+    stride = "1" if os.environ.get("RG_EXHAUSTIVE") == "1" else "16"
+    out = subprocess.run([str(exe), str(min(8, os.cpu_count() or 1)), stride], check=True, capture_output=True,
+                         text=True).stdout
+    rows = {l.split()[0]: l.split()[1:] for l in out.strip().splitlines()}
+    checked, bad, first = rows["monotone"]
+    assert int(checked) >= 0x7f800000 // int(stride) - 65536 * 8
+    assert int(bad) == 0, f"gelu decreases after input 0x{first}"
+    checked, mx, arg, exceeds = rows["negmax"]
+    assert int(exceeds) == 0, f"|gelu(0x{arg})| = 0x{mx} exceeds kGeluNegAbsMax"
+    assert (mx, arg) == ("3e2e1f2c", "bf409c70")  # the bound is attained, at the argmax named in devmath.h
+
+
 def test_program_create_fails_loudly_without_gpu(rg):
     if rg.device_count() > 0:
         pytest.skip("a GPU is present")
