@@ -429,7 +429,10 @@ RG_HD float gelu(float x) {
 //    negative input |gelu(x)| <= kGeluNegAbsMax (both checked exhaustively
 //    on the host, tests/support/gelu_shape_check.cpp).  So over a set of
 //    pre-activations whose largest value xmax has gelu(xmax) >= that bound,
-//    the absmax of the outputs is gelu(xmax).
+//    the absmax of the outputs is gelu(xmax), and any other set whose
+//    gelu(xmax) is below the bound cannot exceed it.  (Below 0 the f32 GELU
+//    is not monotonic on either side of its minimum: rounding in 1 + tanh
+//    makes it wiggle, so no such shortcut exists for negative values.)
 //  * quantization: gelu_approx(x) is within kGeluApproxRel * |x| +
 //    kGeluApproxAbs of gelu(x) for every finite x (checked on the device for
 //    all 2^32 inputs, tests/support/devmath_gpu_check.hip).  Rounding

@@ -760,7 +760,7 @@ __device__ __forceinline__ void epilogue_tile(const int32_t* Cs, const TileCoord
 template <int ACT, bool CAP, int MODE>
 __device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows, float* yrow, int32_t* arow,
                                                    int64_t N, uint32_t col_bytes, float cs, float b, float p,
-                                                   int lane, float amax) {
+                                                   int lane, float amax, bool stream) {
   const __amdgpu_buffer_rsrc_t ry = raw_rsrc(yrow);
   const __amdgpu_buffer_rsrc_t ra = raw_rsrc(arow);
   const uint32_t row_bytes = (uint32_t)N * 4u;
@@ -768,7 +768,12 @@ __device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows
   for (int r = 0; r < rows; r++) {
     const int32_t a = slab[r * big::SLAB_LD + lane];
     const float v = epi_word<ACT, MODE>(a, cs, b, p);
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, (int)col_bytes, (int)(r * row_bytes), 0);
+    // The program's own output is not read again on the device: the
+    // non-temporal hint keeps it from displacing operands in the caches.
+    if (stream)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, (int)col_bytes, (int)(r * row_bytes), 2);
+    else
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ry, (int)col_bytes, (int)(r * row_bytes), 0);
     if (CAP) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)a, ra, (int)col_bytes, (int)(r * row_bytes), 0);
     amax = __builtin_fmaxf(amax, __builtin_fabsf(v));
   }
@@ -799,7 +804,7 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
     const int rows = (int)(M - row0 < 16 ? (M - row0 > 0 ? M - row0 : 0) : 16);
     if (col_ok)
       amax = big_epilogue_slab<ACT, CAP, MODE>(slab, rows, ep.y + row0 * N, CAP ? ep.acc_out + row0 * N : nullptr, N,
-                                               (uint32_t)col * 4u, cs, b, ep.act_param, lane, amax);
+                                               (uint32_t)col * 4u, cs, b, ep.act_param, lane, amax, ep.y_stream != 0);
   }
   return rgmath::fbits(amax);
 }

@@ -1017,6 +1017,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             Epilogue ep;
             ep.bias = op.d_bias.as<float>();
             ep.y = out;
+            ep.y_stream = pl.out_buf == BUF_OUTPUT;
             pre = launch_events_used();
             if (pl.gemv)
               launch_gemv_f32(a, op.d_w.as<float>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
@@ -1040,6 +1041,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             ep.act = op.act;
             ep.act_param = op.act_param;
             ep.y = out;
+            ep.y_stream = pl.out_buf == BUF_OUTPUT;
             pre = launch_events_used();
             if (pl.gemv)
               launch_gemv_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
@@ -1081,6 +1083,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         ep.absmax_in = slot;
         ep.w_scale = op.w_scale;
         ep.y = out;
+        ep.y_stream = pl.out_buf == BUF_OUTPUT;
         ep.absmax_out = emit;
         ep.absmax_out_per_image = 0;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
@@ -1174,6 +1177,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         ep.absmax_in = sl;
         ep.w_scale = op.w_scale;
         ep.y = out;
+        ep.y_stream = pl.out_buf == BUF_OUTPUT;
         ep.absmax_out = emit;
         ep.absmax_out_per_image = pl.emit_per_image;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;

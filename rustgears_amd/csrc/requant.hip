@@ -274,7 +274,7 @@ __device__ __forceinline__ void quantize_stored_flat(const float* y, int8_t* q, 
       const int rr = (k0 + k) * RSTEP;
       const bool ok = rr < rows_left && col_ok;
       v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 0));
+                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 2));
     }
 #pragma unroll
     for (int k = 0; k < BATCH; k++) {
@@ -288,8 +288,10 @@ __device__ __forceinline__ void quantize_stored_flat(const float* y, int8_t* q, 
 // Certified GELU requantization (GELU producer, no capture).  The epilogue
 // keeps and stores the pre-activations x = fl(fl(acc * cs) + b); a lane's
 // exact absmax is gelu(xmax) over its outputs (rgmath::kGeluNegAbsMax and the
-// monotonicity of the f32 GELU on [0, +inf]), with an exact walk over its
-// outputs when gelu(xmax) falls below that bound.  After the barrier each
+// monotonicity of the f32 GELU on [0, +inf]) when that clears the bound, and
+// a lane below it cannot hold the workgroup's absmax unless no lane of the
+// workgroup clears it, in which case the workgroup walks all of its outputs
+// with the exact GELU (cert_exact_absmax).  After the barrier each
 // value is quantized from gelu_approx(x): t = fl(g * inv) and q = round(t)
 // stand when |t - q| + m < 1/2, where m = fl(mc |x|) + m0 covers
 // (kGeluApproxRel |x| + kGeluApproxAbs) inv plus the roundings of t (|t| is
@@ -441,32 +443,51 @@ __device__ __forceinline__ float cert_epilogue(int8_t* smem, v4i (&acc)[FM][4], 
       acc[i][p] = __builtin_bit_cast(v4i, v);
     }
   }
+  // The lane's exact max |gelu| when gelu(xmax) clears the bound, else 0:
+  // such a lane's outputs are all within kGeluNegAbsMax, which any lane of
+  // the workgroup that clears the bound dominates (see cert_exact_absmax).
   const float gx = rgmath::gelu_fast(xmax);
-  if (gx >= thr) return gx;
-  // Rare: the lane's outputs are all small or not finite.  Walk them exactly,
-  // from y (stored here first when this is the kept tile).
+  return gx >= thr ? gx : 0.0f;
+}
+
+// The workgroup's exact max |gelu| over all of its outputs, when no lane's
+// gelu(xmax) cleared the bound (every output of the workgroup is small or not
+// finite; with thr = +inf, the test mode, always): the kept tile's
+// pre-activations go to y beside the stored ones, then the workgroup walks
+// every one of its tiles with the exact GELU.  Every thread calls it; red is
+// NW words of LDS.
+template <int BM, int BN, int NTHREADS, int FM>
+__device__ __forceinline__ float cert_exact_absmax(const v4i (&acc)[FM][4], float* y, int32_t wrow0, int32_t wcol0,
+                                                   int32_t M, int32_t N, const LaneSpan& sp_last, int b, int G,
+                                                   int tiles_m, int tiles_n, int ntile, uint32_t* red, int tid) {
+  constexpr int C4 = BN / 4, RSTEP = NTHREADS / C4;
+  const int lane = tid & 63;
+  store_kept_f32<FM>(acc, y, wrow0, wcol0, N, sp_last, lane);
+  wait_vmcnt<0>();
+  __syncthreads();
   float amax = 0.0f;
-  if (!store) {
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int p = 0; p < 4; p++) {
-        const int ro = i * 16 + p * 4;
-        const bool ok = ro < sp.rows_left && sp.cols_ok;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, acc[i][p]), ry, (int)(ok ? voff : kDropOffset),
-                                               (int)((uint32_t)ro * row_bytes), 0);
-      }
-  }
+  const int c4 = tid % C4, rt = tid / C4;
+  for (int it = 0; it < ntile; it++) {
+    int tm, tn;
+    tile_coords(b + it * G, tiles_m, tiles_n, tm, tn);
+    const int32_t m0 = tm * BM, n0 = tn * BN;
+    if (!(n0 + 4 * c4 < N)) continue;
+    const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(y + (int64_t)m0 * N + n0);
 #pragma unroll 1
-  for (int k = 0; k < FM * 4; k++) {
-    const int ro = (k >> 2) * 16 + (k & 3) * 4;
-    if (!(ro < sp.rows_left && sp.cols_ok)) continue;
-    const v4f v = __builtin_bit_cast(
-        v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)voff, (int)((uint32_t)ro * row_bytes), 0));
+    for (int r = rt; r < BM && m0 + r < M; r += RSTEP) {
+      const v4f v = __builtin_bit_cast(
+          v4f, __builtin_amdgcn_raw_buffer_load_b128(ry, (int)((uint32_t)(r * N + 4 * c4) * 4u), 0, 0));
 #pragma unroll
-    for (int c = 0; c < 4; c++) amax = __builtin_fmaxf(amax, __builtin_fabsf(rgmath::gelu_fast(v[c])));
+      for (int c = 0; c < 4; c++) amax = __builtin_fmaxf(amax, __builtin_fabsf(rgmath::gelu_fast(v[c])));
+    }
   }
-  return amax;
+  const uint32_t m = wave_max_u32(rgmath::fbits(amax));
+  __syncthreads();
+  if (lane == 0) red[tid >> 6] = m;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int w = 1; w < NTHREADS / 64; w++) r = red[w] > r ? red[w] : r;
+  return rgmath::bitsf(r);
 }
 
 // quantize_kept for the certified path: acc holds the pre-activations.
@@ -537,7 +558,7 @@ __device__ __forceinline__ void cert_quantize_stored_flat(const float* y, int8_t
       const int rr = (k0 + k) * RSTEP;
       const bool ok = rr < rows_left && col_ok;
       v[k] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 0));
+                                         ry, (int)(ok ? voff : kDropOffset), (int)((uint32_t)rr * (uint32_t)N * 4u), 2));
     }
 #pragma unroll
     for (int k = 0; k < BATCH; k++) {
@@ -642,9 +663,16 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
     if (lane == 0) blk[2 + wave] = m;
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
+    uint32_t r = blk[2];
+    for (int w = 1; w < NW; w++) r = blk[2 + w] > r ? blk[2 + w] : r;
+    if constexpr (CERT) {
+      // no lane cleared the bound: the exact walk (every thread; rare)
+      if (!(rgmath::bitsf(r) >= cert_thr))
+        r = rgmath::fbits(cert_exact_absmax<BM, BN, NW * 64, FM>(acc, ep.y, m0 + wrow, n0 + wcolw, M, N,
+                                                                  lane_span(m0 + wrow, n0 + wcolw, M, N, lane), b, G,
+                                                                  sh.tiles_m, sh.tiles_n, ntile, blk + 2, tid));
+    }
     if (tid == 0) {
-      uint32_t r = blk[2];
-      for (int w = 1; w < NW; w++) r = blk[2 + w] > r ? blk[2 + w] : r;
       if (r) atomicMax(ep.absmax_out + (b & (kSpread - 1)) * kSpreadStride, r);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the atomic has completed before the arrival
     }
@@ -807,7 +835,7 @@ __device__ __forceinline__ v4f iq_load(__amdgpu_buffer_rsrc_t rx, uint32_t r, ui
   const uint32_t base = (r * (uint32_t)s.K + c0) * 4u;  // used only in bounds (input < 2^31 bytes)
   if constexpr (VEC) {
     const bool ok = row_ok && c0 < (uint32_t)s.K;  // K % 4 == 0: a unit is all in or all out
-    return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? base : kDropOffset), 0, 0));
+    return __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(ok ? base : kDropOffset), 0, 2));
   } else {
     v4f v;
 #pragma unroll

@@ -47,6 +47,7 @@ struct Epilogue {
   uint32_t* absmax_out = nullptr;      // nullable: absmax of y for the next op
   int absmax_out_per_image = 0;        // 1: slot per image; 0: spread per-tensor slot
   int32_t* acc_out = nullptr;          // nullable: i32 accumulator capture
+  int y_stream = 0;                    // 1: y is the program's output, stored with the non-temporal hint
 };
 
 // Requantization fused into a producing Linear's GEMM (requant.hip): the

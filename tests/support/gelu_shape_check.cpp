@@ -82,5 +82,6 @@ int main(int argc, char** argv) {
   }
   printf("negmax %llu %08x %08x %d\n", (unsigned long long)nc, m, am,
          (int)(m > rgmath::fbits(rgmath::kGeluNegAbsMax)));
+
   return 0;
 }
