@@ -784,11 +784,67 @@ __device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows
 // time and stores it row-major: lane l owns column n0 + wn*64 + l, so each
 // store instruction writes 256 contiguous bytes.  The bias and scale were
 // loaded before the K loop.
+// FP16 hand-off (ep.h_out): the same slabs read back with 4 consecutive
+// columns per lane; each output y = act(round_fp16(acc + b)) (npu.rs:442)
+// becomes the consumer's binary16 operand fp16_bits(round_fp16(y)), exactly
+// what the consumer's own conversion (half_rows_kernel) would write, with the
+// operand's zero padding for rows past M and columns past N.  N % 4 == 0, so
+// a lane's 4 columns are all outputs or all padding; columns at or past ldh
+// are not part of the operand.  y (when not null) gets the f32 outputs.
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+template <int ACT, int FM>
+__device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4i (&acc)[FM][4], int64_t m0,
+                                                         int64_t n0, int64_t M, int64_t N, const Epilogue& ep, int wm,
+                                                         int wn, int lane) {
+  const int sub = lane >> 4, c4 = (lane & 15) * 4;
+  const int64_t row0 = m0 + wm * (16 * FM), col0 = n0 + wn * 64;
+  const int64_t col = col0 + c4;
+  const bool col_ok = col < N, h_ok = col < ep.ldh;
+  const float4 b4 = col_ok ? *reinterpret_cast<const float4*>(ep.bias + col) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+  // wave-uniform bases, 32-bit lane offsets (the plan bounds the operand and
+  // output below 2^31 bytes per 128 rows), row offsets in the scalar offset
+  const __amdgpu_buffer_rsrc_t rh = raw_rsrc(ep.h_out + row0 * ep.ldh + col0);
+  const uint32_t hoff = (uint32_t)((sub * ep.ldh + c4) * 2), hrow = (uint32_t)ep.ldh * 2u;
+  const int32_t rows_left = (int32_t)(M - row0 - sub);  // row 16 i + 4 p (+ sub) is an output iff 16 i + 4 p < rows_left
+#pragma unroll
+  for (int i = 0; i < FM; i++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int ro = i * 16 + p * 4;
+      const v4i a = *reinterpret_cast<const v4i*>(slab + (p * 4 + sub) * big::SLAB_LD + c4);
+      const bool ok = ro < rows_left && col_ok;
+      v4f v;
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[c] = epi_word<ACT, kModeF16>(a[c], 1.0f, bb[c], ep.act_param);
+      if (h_ok) {
+        const uint32_t lo = ok ? half2_of(v[0], v[1]) : 0u, hi = ok ? half2_of(v[2], v[3]) : 0u;
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, make_uint2(lo, hi)), rh, (int)hoff,
+                                              (int)((uint32_t)ro * hrow), 0);
+      }
+      const int64_t row = row0 + ro + sub;
+      if (ep.y && ok) *reinterpret_cast<v4f*>(ep.y + row * N + col) = v;
+      if (ep.acc_out && ok) *reinterpret_cast<v4i*>(ep.acc_out + row * N + col) = a;
+    }
+  }
+}
+
 template <int ACT, bool CAP, int FM, int MODE>
 __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[FM][4], int64_t m0, int64_t n0,
                                                  int64_t M, int64_t N, float cs, float b, const Epilogue& ep,
                                                  int wave, int wm, int wn, int lane) {
   int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
+  if constexpr (MODE == kModeF16) {
+    if (ep.h_out) {
+      big_epilogue_f16_handoff<ACT, FM>(slab, acc, m0, n0, M, N, ep, wm, wn, lane);
+      return 0u;
+    }
+  }
   float amax = 0.0f;
   const int64_t col = n0 + wn * 64 + lane;
   // Every lane stages its accumulators (the slab is shared by the wave);

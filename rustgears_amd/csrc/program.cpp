@@ -147,6 +147,9 @@ struct OpPlan {
   // kernel's barrier words in the slot set, or -1 for the absmax + quantize
   // kernel pair.
   int64_t iq_sync_base = -1;
+  // FP16 Linear -> FP16 Linear: the producer's GEMM epilogue writes the
+  // consumer's binary16 operand (q_ready / q_in of the consumer as above).
+  bool handoff = false;
 };
 
 struct Plan {
@@ -794,6 +797,31 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     cpl.q_in = pl.q_in ^ 1;
     any_requant = true;
   }
+  // FP16: a Linear on the unsplit MFMA GEMM whose next computing op is an
+  // FP16 Linear on the same rows hands it its binary16 operand from the GEMM
+  // epilogue, so the consumer runs no conversion pass (RGNPU_F16_HANDOFF=0
+  // turns this off).
+  const char* hoff = getenv("RGNPU_F16_HANDOFF");
+  const bool handoff_on = !(hoff && atoi(hoff) == 0);
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_FP16 && handoff_on; i++) {
+    const Op& op = *P->ops[i];
+    OpPlan& pl = plan->ops[i];
+    if (op.kind != OP_LINEAR || op.diag || pl.gemv || op.out_f <= kNarrowMaxN || pl.rows <= 0 || op.out_f % 4) continue;
+    if (choose_gemm(pl.Mpad, op.Npad, 2 * op.Kpad).splits != 1) continue;
+    size_t j = i + 1;
+    while (j < nops && P->ops[j]->kind == OP_FLATTEN) j++;
+    if (j >= nops || P->ops[j]->kind != OP_LINEAR) continue;
+    const Op& cop = *P->ops[j];
+    OpPlan& cpl = plan->ops[j];
+    if (cop.diag || cop.in_f != op.out_f || cpl.rows != pl.rows || cpl.gemv || cpl.Mpad != pl.Mpad ||
+        cop.Kpad > op.Npad)
+      continue;
+    pl.handoff = true;
+    pl.consumer = (int)j;
+    cpl.q_ready = true;
+    cpl.q_in = pl.q_in ^ 1;
+    any_requant = true;  // the second operand buffer
+  }
   // A Linear that quantizes its own input does so in one pass when the
   // shapes fit the kernel's 32-bit offsets.
   for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
@@ -1034,14 +1062,20 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           if (op.diag) {
             launch_affine_f16(in, pl.in_len, op.in_f, op.d_scale.as<float>(), op.d_bias.as<float>(), out, s);
           } else if (pl.rows > 0) {
-            uint16_t* h = plan.q.as<uint16_t>();
-            launch_half_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, h, s);
+            uint16_t* h = pl.q_in ? plan.q_alt.as<uint16_t>() : plan.q.as<uint16_t>();
+            if (!pl.q_ready) launch_half_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, h, s);
             Epilogue ep;
             ep.bias = op.d_bias.as<float>();
             ep.act = op.act;
             ep.act_param = op.act_param;
             ep.y = out;
             ep.y_stream = pl.out_buf == BUF_OUTPUT;
+            if (pl.handoff) {
+              const OpPlan& cpl = plan.ops[(size_t)pl.consumer];
+              ep.h_out = cpl.q_in ? plan.q_alt.as<uint16_t>() : plan.q.as<uint16_t>();
+              ep.ldh = P->ops[(size_t)pl.consumer]->Kpad;
+              if (!cap) ep.y = nullptr;  // nothing reads the f32 output
+            }
             pre = launch_events_used();
             if (pl.gemv)
               launch_gemv_f16(h, op.d_w.as<uint16_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);

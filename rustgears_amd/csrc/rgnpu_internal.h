@@ -48,6 +48,11 @@ struct Epilogue {
   int absmax_out_per_image = 0;        // 1: slot per image; 0: spread per-tensor slot
   int32_t* acc_out = nullptr;          // nullable: i32 accumulator capture
   int y_stream = 0;                    // 1: y is the program's output, stored with the non-temporal hint
+  // FP16 Linear -> FP16 Linear: the consumer's binary16 operand [Mpad, ldh]
+  // (zero padded), written by this GEMM's epilogue in place of the consumer's
+  // conversion pass; y may then be null (no f32 output wanted).
+  uint16_t* h_out = nullptr;
+  int64_t ldh = 0;
 };
 
 // Requantization fused into a producing Linear's GEMM (requant.hip): the

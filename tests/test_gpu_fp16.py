@@ -237,3 +237,42 @@ def test_fp16_random_models(rg, ref, seed):
     from test_gpu_parity import _random_model
     layers, x = _random_model(1000 + seed)
     check_per_op(rg, ref, layers, x, f"random model {seed}")
+
+
+HANDOFF_CASES = [
+    # (name, dims, act, rows): the tile shape of the producer GEMMs in the comment
+    ("stack 256x256 gelu", [4096, 4096, 4096, 4096], "gelu", 8192),  # S's shape, 3 hand-offs
+    ("256x128 relu ragged", [1000, 3000, 2004, 20], "relu", 2600),    # then 128x128; N = 2004 pads to 2048
+    ("128x128 tanh", [700, 1024, 516, 300], "tanh", 2048),            # 1024 -> 516 splits K: converts
+]
+
+
+@pytest.mark.parametrize("name,dims,act,rows", HANDOFF_CASES, ids=[c[0] for c in HANDOFF_CASES])
+def test_fp16_operand_handoff_is_bit_identical(rg, monkeypatch, name, dims, act, rows):
+    """An FP16 Linear whose next op is an FP16 Linear on the same rows writes
+    that Linear's binary16 operand from its GEMM epilogue (the consumer's
+    conversion pass is gone): outputs bit-identical to RGNPU_F16_HANDOFF=0,
+    and a consumer fed this way launches nothing before its GEMM."""
+    from rustgears_amd import nn
+    rg.manual_seed(rows + len(dims))
+    act_cls = {"gelu": nn.Gelu, "relu": nn.Relu, "tanh": nn.Tanh}[act]
+    m = nn.Sequential()
+    for a, b in zip(dims[:-1], dims[1:]):
+        m.add(nn.Linear(a, b)).add(act_cls())
+    layers = m.export()
+    x = rg.randn([rows, dims[0]])
+    outs, profs = {}, {}
+    for mode in ("1", "0"):
+        monkeypatch.setenv("RGNPU_F16_HANDOFF", mode)
+        print(f"[fp16-handoff] {name} mode {mode}", flush=True)
+        sess = make_session(rg, layers)
+        outs[mode] = sess.run(x)
+        y2 = sess.run(x)
+        profs[mode] = sess.last_npu_profile()
+        sess.close()
+        assert_bitexact_f32(y2, outs[mode], f"{name} mode {mode} second run")
+    assert_bitexact_f32(outs["1"], outs["0"], f"{name}: hand-off vs conversion pass")
+    gemms = [r for r in profs["1"].records if "Gemm" in r.op]
+    assert gemms[1].duration_ns == gemms[1].kernel_ns, gemms  # no conversion before the second GEMM
+    gemms0 = [r for r in profs["0"].records if "Gemm" in r.op]
+    assert gemms0[1].duration_ns > gemms0[1].kernel_ns, gemms0
