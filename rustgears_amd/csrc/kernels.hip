@@ -790,7 +790,8 @@ __device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows
 // what the consumer's own conversion (half_rows_kernel) would write, with the
 // operand's zero padding for rows past M and columns past N.  N % 4 == 0, so
 // a lane's 4 columns are all outputs or all padding; columns at or past ldh
-// are not part of the operand.  y (when not null) gets the f32 outputs.
+// are not part of the operand.  No f32 output is stored (capture runs do not
+// hand off).
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 template <int ACT, int FM>
@@ -814,7 +815,9 @@ __device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) slab[((lane >> 4) * 4 + r) * big::SLAB_LD + j * 16 + (lane & 15)] = acc[i][j][r];
-#pragma unroll
+    // the rows are read back from the slab in a rolled loop: acc is indexed
+    // only by the unrolled staging above, so it stays in registers
+#pragma unroll 1
     for (int p = 0; p < 4; p++) {
       const int ro = i * 16 + p * 4;
       const v4i a = *reinterpret_cast<const v4i*>(slab + (p * 4 + sub) * big::SLAB_LD + c4);
@@ -827,9 +830,6 @@ __device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, make_uint2(lo, hi)), rh, (int)hoff,
                                               (int)((uint32_t)ro * hrow), 0);
       }
-      const int64_t row = row0 + ro + sub;
-      if (ep.y && ok) *reinterpret_cast<v4f*>(ep.y + row * N + col) = v;
-      if (ep.acc_out && ok) *reinterpret_cast<v4i*>(ep.acc_out + row * N + col) = a;
     }
   }
 }

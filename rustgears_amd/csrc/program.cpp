@@ -1062,19 +1062,21 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           if (op.diag) {
             launch_affine_f16(in, pl.in_len, op.in_f, op.d_scale.as<float>(), op.d_bias.as<float>(), out, s);
           } else if (pl.rows > 0) {
+            // Capture runs store every f32 output and convert every input
+            // (no hand-off); each op still reads its own operand buffer.
             uint16_t* h = pl.q_in ? plan.q_alt.as<uint16_t>() : plan.q.as<uint16_t>();
-            if (!pl.q_ready) launch_half_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, h, s);
+            if (!pl.q_ready || cap) launch_half_rows(in, pl.rows, op.K, pl.Mpad, op.Kpad, h, s);
             Epilogue ep;
             ep.bias = op.d_bias.as<float>();
             ep.act = op.act;
             ep.act_param = op.act_param;
             ep.y = out;
             ep.y_stream = pl.out_buf == BUF_OUTPUT;
-            if (pl.handoff) {
+            if (pl.handoff && !cap) {
               const OpPlan& cpl = plan.ops[(size_t)pl.consumer];
               ep.h_out = cpl.q_in ? plan.q_alt.as<uint16_t>() : plan.q.as<uint16_t>();
               ep.ldh = P->ops[(size_t)pl.consumer]->Kpad;
-              if (!cap) ep.y = nullptr;  // nothing reads the f32 output
+              ep.y = nullptr;  // nothing reads the f32 output
             }
             pre = launch_events_used();
             if (pl.gemv)

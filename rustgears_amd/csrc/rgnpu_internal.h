@@ -50,7 +50,7 @@ struct Epilogue {
   int y_stream = 0;                    // 1: y is the program's output, stored with the non-temporal hint
   // FP16 Linear -> FP16 Linear: the consumer's binary16 operand [Mpad, ldh]
   // (zero padded), written by this GEMM's epilogue in place of the consumer's
-  // conversion pass; y may then be null (no f32 output wanted).
+  // conversion pass; no f32 output is stored then.
   uint16_t* h_out = nullptr;
   int64_t ldh = 0;
 };
