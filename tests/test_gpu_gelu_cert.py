@@ -14,8 +14,9 @@ the results bit for bit against the oracle:
   thousand through the per-wave LDS queue of exact fallbacks; 2 every value
   uncertain (each queue overflows: the exact re-walk); 0 the exact GELU
   everywhere.  Also with deferral to the finisher;
-* tensors whose absmax comes from negative pre-activations (every lane takes
-  the exact absmax walk), and a mix of lanes that do and do not;
+* tensors whose absmax comes from negative pre-activations (no lane clears
+  the bound, so every workgroup takes the exact absmax walk), and a mix of
+  workgroups that do and do not;
 * NaN and -inf pre-activations (bias columns), whose GELU is NaN: ignored by
   the absmax, quantized to 0.
 """
