@@ -794,10 +794,71 @@ __device__ __forceinline__ float big_epilogue_slab(const int32_t* slab, int rows
 // hand off).
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
-template <int ACT, int FM>
-__device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4i (&acc)[FM][4], int64_t m0,
-                                                         int64_t n0, int64_t M, int64_t N, const Epilogue& ep, int wm,
-                                                         int wn, int lane) {
+// The binary16 operand of an FP16 output value (what half_rows_kernel writes).
+__device__ __forceinline__ uint32_t h16(float y) { return rgmath::fp16_bits(rgmath::round_fp16(y)); }
+
+// Certified GELU for the hand-off (ACT == GELU): the operand of
+// gelu(pre) is h16 of it, and h16 never decreases (as the value it encodes)
+// and never gives -0 over the finite f32 values (host check,
+// tests/support/gelu_shape_check.cpp).  gelu_approx(pre) is within
+// kGeluApproxRel |pre| + kGeluApproxAbs of gelu(pre) (device check), so when
+// h16 agrees at both ends of that interval, widened for the roundings of its
+// ends, it is the exact value's operand.  pre = round_fp16(acc + b) is always
+// finite.  The values the test cannot decide go to a per-wave queue in LDS
+// and get the exact GELU after the walk; a queue that overflows sends the
+// wave through the exact walk again.
+namespace f16c {
+constexpr int kQueue = 512;        // entries per wave
+constexpr int kQueueBase = 36864;  // bytes from the LDS array's start: past the 8 epilogue slabs
+static_assert(kQueueBase >= 8 * big::SLAB, "the queues follow the slabs");
+}  // namespace f16c
+
+struct F16Cert {
+  float c1, c2, c3;  // interval half-width e = c1 |pre| + c3 |g| + c2
+};
+
+__device__ __forceinline__ F16Cert f16_cert_const(int mode) {
+  F16Cert c;
+  c.c1 = rgmath::kGeluApproxRel * 1.001f;
+  c.c2 = mode == 2 ? __builtin_inff() : rgmath::kGeluApproxAbs * 2.0f;
+  c.c3 = mode == 3 ? 0x1p-18f : 0x1p-22f;  // 2^-22: the roundings of g -+ e; mode 3 queues ~1% of the values
+  return c;
+}
+
+__device__ __forceinline__ uint32_t cert_h16(float pre, const F16Cert& c, bool& ok) {
+  const float g = rgmath::gelu_approx(pre);
+  const float e = __builtin_fmaf(c.c1, __builtin_fabsf(pre), __builtin_fmaf(c.c3, __builtin_fabsf(g), c.c2));
+  const uint32_t lo = h16(g - e), hi = h16(g + e);
+  ok = lo == hi;
+  return lo;
+}
+
+__device__ __forceinline__ void f16_push(uint32_t* qx, uint32_t* qo, uint32_t& n, bool need, float pre,
+                                         uint32_t off) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
+  if (m == 0) return;
+  if (need) {
+    const uint32_t pos = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (pos < (uint32_t)f16c::kQueue) {
+      qx[pos] = __float_as_uint(pre);
+      qo[pos] = off;
+    }
+  }
+  n += (uint32_t)__builtin_popcountll(m);
+}
+
+// FP16 hand-off (ep.h_out): the same slabs read back with 4 consecutive
+// columns per lane; each output y = act(round_fp16(acc + b)) (npu.rs:442)
+// becomes the consumer's binary16 operand fp16_bits(round_fp16(y)), exactly
+// what the consumer's own conversion (half_rows_kernel) would write, with the
+// operand's zero padding for rows past M and columns past N.  N % 4 == 0, so
+// a lane's 4 columns are all outputs or all padding; columns at or past ldh
+// are not part of the operand.  No f32 output is stored (capture runs do not
+// hand off).  CERT: the certified GELU above.
+template <int ACT, int FM, bool CERT>
+__device__ __forceinline__ void big_epilogue_f16_handoff(int8_t* smem, int32_t* slab, const v4i (&acc)[FM][4],
+                                                         int64_t m0, int64_t n0, int64_t M, int64_t N,
+                                                         const Epilogue& ep, int wave, int wm, int wn, int lane) {
   const int sub = lane >> 4, c4 = (lane & 15) * 4;
   const int64_t row0 = m0 + wm * (16 * FM), col0 = n0 + wn * 64;
   const int64_t col = col0 + c4;
@@ -809,6 +870,10 @@ __device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4
   const __amdgpu_buffer_rsrc_t rh = raw_rsrc(ep.h_out + row0 * ep.ldh + col0);
   const uint32_t hoff = (uint32_t)((sub * ep.ldh + c4) * 2), hrow = (uint32_t)ep.ldh * 2u;
   const int32_t rows_left = (int32_t)(M - row0 - sub);  // row 16 i + 4 p (+ sub) is an output iff 16 i + 4 p < rows_left
+  uint32_t* const qx = reinterpret_cast<uint32_t*>(smem + f16c::kQueueBase) + wave * 2 * f16c::kQueue;
+  uint32_t* const qo = qx + f16c::kQueue;
+  uint32_t n = 0;
+  const F16Cert cc = f16_cert_const(ep.gelu_cert);
 #pragma unroll
   for (int i = 0; i < FM; i++) {
 #pragma unroll
@@ -822,15 +887,45 @@ __device__ __forceinline__ void big_epilogue_f16_handoff(int32_t* slab, const v4
       const int ro = i * 16 + p * 4;
       const v4i a = *reinterpret_cast<const v4i*>(slab + (p * 4 + sub) * big::SLAB_LD + c4);
       const bool ok = ro < rows_left && col_ok;
-      v4f v;
+      uint32_t hv[4];
+      if constexpr (CERT) {
+        bool o[4];
+        float pre[4];
 #pragma unroll
-      for (int c = 0; c < 4; c++) v[c] = epi_word<ACT, kModeF16>(a[c], 1.0f, bb[c], ep.act_param);
+        for (int c = 0; c < 4; c++) {
+          pre[c] = rgmath::round_fp16(__int_as_float(a[c]) + bb[c]);
+          hv[c] = cert_h16(pre[c], cc, o[c]);
+        }
+        const bool valid = ok && h_ok;
+        if (__builtin_amdgcn_ballot_w64(valid && !(o[0] && o[1] && o[2] && o[3]))) {
+          const uint32_t off = hoff + (uint32_t)ro * hrow;
+#pragma unroll
+          for (int c = 0; c < 4; c++) f16_push(qx, qo, n, valid && !o[c], pre[c], off + 2u * c);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) hv[c] = h16(epi_word<ACT, kModeF16>(a[c], 1.0f, bb[c], ep.act_param));
+      }
       if (h_ok) {
-        const uint32_t lo = ok ? half2_of(v[0], v[1]) : 0u, hi = ok ? half2_of(v[2], v[3]) : 0u;
+        const uint32_t lo = ok ? (hv[0] | (hv[1] << 16)) : 0u, hi = ok ? (hv[2] | (hv[3] << 16)) : 0u;
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, make_uint2(lo, hi)), rh, (int)hoff,
                                               (int)((uint32_t)ro * hrow), 0);
       }
     }
+  }
+  if constexpr (CERT) {
+    if (n == 0) return;
+    if (n > (uint32_t)f16c::kQueue) {
+      // overflow: the exact walk again (acc is unchanged)
+      big_epilogue_f16_handoff<ACT, FM, false>(smem, slab, acc, m0, n0, M, N, ep, wave, wm, wn, lane);
+      return;
+    }
+    // the walk's word stores have completed, so these 2-byte stores land
+    // after them whichever lane makes them
+    wait_vmcnt<0>();
+    for (uint32_t j = (uint32_t)lane; j < n; j += 64)
+      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)h16(rgmath::gelu_fast(__uint_as_float(qx[j]))), rh,
+                                            (int)qo[j], 0, 0);
   }
 }
 
@@ -841,7 +936,13 @@ __device__ __forceinline__ uint32_t big_epilogue(int8_t* smem, const v4i (&acc)[
   int32_t* slab = reinterpret_cast<int32_t*>(smem + wave * big::SLAB);
   if constexpr (MODE == kModeF16) {
     if (ep.h_out) {
-      big_epilogue_f16_handoff<ACT, FM>(slab, acc, m0, n0, M, N, ep, wm, wn, lane);
+      if constexpr (ACT == rgmath::ACT_GELU) {
+        if (ep.gelu_cert) {
+          big_epilogue_f16_handoff<ACT, FM, true>(smem, slab, acc, m0, n0, M, N, ep, wave, wm, wn, lane);
+          return 0u;
+        }
+      }
+      big_epilogue_f16_handoff<ACT, FM, false>(smem, slab, acc, m0, n0, M, N, ep, wave, wm, wn, lane);
       return 0u;
     }
   }
@@ -884,6 +985,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
   static_assert(BM == 16 * FM * WAVES_M && BN == 64 * WAVES_N, "wave tile is (16 FM) x 64");
   constexpr int ST = (BM + BN) * BK;
   static_assert(NW * SLAB <= STAGES * ST, "epilogue slabs reuse the ring");
+  static_assert(MODE != kModeF16 || f16c::kQueueBase + NW * 8 * f16c::kQueue <= STAGES * ST,
+                "the FP16 hand-off queues fit in the ring");
   __shared__ __attribute__((aligned(1024))) int8_t smem[STAGES * ST];
   // wave index read through a scalar register: the compiler then keeps the
   // wave's tile coordinates and row bases scalar

@@ -1076,6 +1076,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
               const OpPlan& cpl = plan.ops[(size_t)pl.consumer];
               ep.h_out = cpl.q_in ? plan.q_alt.as<uint16_t>() : plan.q.as<uint16_t>();
               ep.ldh = P->ops[(size_t)pl.consumer]->Kpad;
+              ep.gelu_cert = plan.gelu_cert;
               ep.y = nullptr;  // nothing reads the f32 output
             }
             pre = launch_events_used();

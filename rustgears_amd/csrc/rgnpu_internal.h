@@ -53,6 +53,7 @@ struct Epilogue {
   // conversion pass; no f32 output is stored then.
   uint16_t* h_out = nullptr;
   int64_t ldh = 0;
+  int gelu_cert = 0;  // with h_out and GELU: 1 certified (2, 3 test modes as in Requant), 0 exact
 };
 
 // Requantization fused into a producing Linear's GEMM (requant.hip): the

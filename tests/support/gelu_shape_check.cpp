@@ -7,8 +7,11 @@
 //   2. over every negative f32 (finite or -inf) |gelu(x)| is at most
 //      rgmath::kGeluNegAbsMax (NaN results, which the absmax ignores, are
 //      skipped), and that bound is attained.
-// Prints "monotone <checked> <violations> <first_bad_hex>" and
-// "negmax <checked> <max_bits_hex> <argmax_hex> <exceeds_bound>".
+//   3. (the certified FP16 hand-off) fp16_bits(round_fp16(y)) is monotonic
+//      in y over the finite f32 values and never gives -0.
+// Prints "monotone <checked> <violations> <first_bad_hex>",
+// "negmax <checked> <max_bits_hex> <argmax_hex> <exceeds_bound>" and
+// "fp16mono <checked pairs> <violations> <first_bad_hex>".
 // Usage: gelu_shape_check <threads> [stride]: with stride s > 1 only every
 // s-th block of 2^16 consecutive bit patterns is walked (all of them at 1).
 #include <cmath>
@@ -83,5 +86,48 @@ int main(int argc, char** argv) {
   printf("negmax %llu %08x %08x %d\n", (unsigned long long)nc, m, am,
          (int)(m > rgmath::fbits(rgmath::kGeluNegAbsMax)));
 
+  // 3. the FP16 operand of a value, h(y) = fp16_bits(round_fp16(y)), never
+  // decreases (as the binary16 value it encodes) over the finite f32 values
+  // in increasing order, and is never -0: equal h at both ends of an interval
+  // then means equal h inside it.  Walk: bits 0xff7fffff (-max) down to
+  // 0x80000000 (-0), then 0 up to 0x7f7fffff (+max), as one sequence of
+  // 2^32 - 2^24 - 1 steps (-0 and +0 are one value).
+  auto h_key = [](float y) -> int32_t {
+    const uint16_t h = rgmath::fp16_bits(rgmath::round_fp16(y));
+    return (h & 0x8000u) ? -(int32_t)(h & 0x7fffu) - (h == 0x8000u ? 1 << 20 : 0) : (int32_t)h;  // -0 fails
+  };
+  auto seq = [](uint64_t k) -> uint32_t {  // k-th finite f32 in increasing order
+    const uint64_t nneg = 0xff7fffffull - 0x80000000ull + 1;  // -max .. -0
+    return k < nneg ? (uint32_t)(0xff7fffffull - k) : (uint32_t)(k - nneg + 1);  // then +min .. +max (skip +0)
+  };
+  const uint64_t total = (0xff7fffffull - 0x80000000ull + 1) + 0x7f7fffffull;
+  th.clear();
+  std::vector<uint64_t> hchk(nt, 0), hbad(nt, 0);
+  std::vector<uint32_t> hfirst(nt, 0xffffffffu);
+  for (int w = 0; w < nt; w++)
+    th.emplace_back([&, w] {
+      const uint64_t lo = (total - 1) * w / nt, hi = (total - 1) * (w + 1) / nt;  // pairs (k, k+1)
+      int32_t prev = h_key(rgmath::bitsf(seq(lo)));
+      for (uint64_t k = lo; k < hi; k++) {
+        if (!walked(k)) {
+          k = (k / kBlock + 1) * kBlock - 1;
+          if (k + 1 < hi) prev = h_key(rgmath::bitsf(seq(k + 1)));
+          continue;
+        }
+        const int32_t next = h_key(rgmath::bitsf(seq(k + 1)));
+        hchk[w]++;
+        if (!(next >= prev) && hbad[w]++ == 0) hfirst[w] = seq(k);
+        prev = next;
+      }
+    });
+  for (auto& t : th) t.join();
+  uint64_t hc = 0, hb = 0;
+  uint32_t hf = 0xffffffffu;
+  for (int w = 0; w < nt; w++) {
+    hc += hchk[w];
+    hb += hbad[w];
+    if (hfirst[w] < hf) hf = hfirst[w];
+  }
+  printf("fp16mono %llu %llu %08x\n", (unsigned long long)hc, (unsigned long long)hb, hf);
   return 0;
 }

@@ -252,7 +252,11 @@ def test_fp16_operand_handoff_is_bit_identical(rg, monkeypatch, name, dims, act,
     """An FP16 Linear whose next op is an FP16 Linear on the same rows writes
     that Linear's binary16 operand from its GEMM epilogue (the consumer's
     conversion pass is gone): outputs bit-identical to RGNPU_F16_HANDOFF=0,
-    and a consumer fed this way launches nothing before its GEMM."""
+    and a consumer fed this way launches nothing before its GEMM.  With GELU
+    the hand-off certifies the operand from gelu_approx: every mode of
+    RGNPU_GELU_CERT (1 certified, 3 a margin that queues ~1% of the values
+    for the exact GELU, 2 every value uncertain so each wave redoes its walk
+    exactly, 0 exact) must give the same bits."""
     from rustgears_amd import nn
     rg.manual_seed(rows + len(dims))
     act_cls = {"gelu": nn.Gelu, "relu": nn.Relu, "tanh": nn.Tanh}[act]
@@ -261,18 +265,22 @@ def test_fp16_operand_handoff_is_bit_identical(rg, monkeypatch, name, dims, act,
         m.add(nn.Linear(a, b)).add(act_cls())
     layers = m.export()
     x = rg.randn([rows, dims[0]])
+    runs = [("0", "1"), ("1", "1")] + ([("1", "3"), ("1", "2"), ("1", "0")] if act == "gelu" else [])
     outs, profs = {}, {}
-    for mode in ("1", "0"):
-        monkeypatch.setenv("RGNPU_F16_HANDOFF", mode)
-        print(f"[fp16-handoff] {name} mode {mode}", flush=True)
+    for handoff, cert in runs:
+        monkeypatch.setenv("RGNPU_F16_HANDOFF", handoff)
+        monkeypatch.setenv("RGNPU_GELU_CERT", cert)
+        print(f"[fp16-handoff] {name} handoff {handoff} cert {cert}", flush=True)
         sess = make_session(rg, layers)
-        outs[mode] = sess.run(x)
+        y = sess.run(x)
         y2 = sess.run(x)
-        profs[mode] = sess.last_npu_profile()
+        profs[handoff, cert] = sess.last_npu_profile()
         sess.close()
-        assert_bitexact_f32(y2, outs[mode], f"{name} mode {mode} second run")
-    assert_bitexact_f32(outs["1"], outs["0"], f"{name}: hand-off vs conversion pass")
-    gemms = [r for r in profs["1"].records if "Gemm" in r.op]
+        assert_bitexact_f32(y2, y, f"{name} handoff {handoff} cert {cert} second run")
+        outs[handoff, cert] = y
+    for key in runs[1:]:
+        assert_bitexact_f32(outs[key], outs["0", "1"], f"{name}: hand-off (cert {key[1]}) vs conversion pass")
+    gemms = [r for r in profs["1", "1"].records if "Gemm" in r.op]
     assert gemms[1].duration_ns == gemms[1].kernel_ns, gemms  # no conversion before the second GEMM
-    gemms0 = [r for r in profs["0"].records if "Gemm" in r.op]
+    gemms0 = [r for r in profs["0", "1"].records if "Gemm" in r.op]
     assert gemms0[1].duration_ns > gemms0[1].kernel_ns, gemms0

@@ -215,8 +215,10 @@ def test_gelu_shape_for_certified_requantization(tmp_path):
     reference's glibc form on every input) that let the INT8 GELU
     requantization take the tensor absmax from the largest pre-activation:
     it never decreases on [0, +inf], and |gelu(x)| <= kGeluNegAbsMax for every
-    negative x, with equality at x = -0x1.8138e0p-1.  Every 16th block of 2^16
-    consecutive bit patterns (all of them with RG_EXHAUSTIVE=1)."""
+    negative x, with equality at x = -0x1.8138e0p-1; and, for the certified
+    FP16 hand-off, that fp16_bits(round_fp16(y)) is monotonic over the finite
+    f32 values and never -0.  Every 16th block of 2^16 consecutive bit
+    patterns (all of them with RG_EXHAUSTIVE=1)."""
     exe = tmp_path / "gshape"
     src = os.path.join(ROOT, "tests", "support", "gelu_shape_check.cpp")
     subprocess.run(["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-pthread", "-o", str(exe), src, "-lm"],
@@ -231,6 +233,9 @@ def test_gelu_shape_for_certified_requantization(tmp_path):
     checked, mx, arg, exceeds = rows["negmax"]
     assert int(exceeds) == 0, f"|gelu(0x{arg})| = 0x{mx} exceeds kGeluNegAbsMax"
     assert (mx, arg) == ("3e2e1f2c", "bf409c70")  # the bound is attained, at the argmax named in devmath.h
+    checked, bad, first = rows["fp16mono"]
+    assert int(checked) >= 0xff000000 // int(stride) - 65536 * 8
+    assert int(bad) == 0, f"fp16_bits(round_fp16(y)) decreases (or gives -0) after input 0x{first}"
 
 
 def test_program_create_fails_loudly_without_gpu(rg):
