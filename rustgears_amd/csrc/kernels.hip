@@ -432,6 +432,15 @@ __global__ __launch_bounds__(256) void nlo_to_nchw_kernel(const float* __restric
 // FP32: multiply, then add (no contraction); the output is sum + bias (the
 // activation is a layer of its own).  The weights of one output channel are
 // read at a wave-uniform address.
+// FP16 direct conv outputs: act(round_fp16(acc + bias)) per output channel.
+template <int ACT, int OMAX>
+__device__ __forceinline__ void conv_direct_store_f16(const float (&acc)[OMAX], const float* __restrict__ bias,
+                                                      float* yb, int64_t L, int O, float act_param) {
+#pragma unroll
+  for (int o = 0; o < OMAX; o++)
+    if (o < O) yb[(int64_t)o * L] = act_fixed<ACT>(rgmath::round_fp16(acc[o] + bias[o]), act_param);
+}
+
 template <int OMAX, int MODE>
 __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restrict__ x, const void* __restrict__ wv,
                                                           const float* __restrict__ bias, float* __restrict__ y,
@@ -497,17 +506,24 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restric
       }
     }
   float* yb = y + b * (int64_t)O * L + pix;
-#pragma unroll
-  for (int o = 0; o < OMAX; o++) {
-    if (o >= O) break;
-    float v;
-    if constexpr (MODE == kModeF16) {
-      const float pre = rgmath::round_fp16(acc[o] + bias[o]);
-      v = rgmath::act_apply(act, act_param, pre);
-    } else {
-      v = acc[o] + bias[o];
+  if constexpr (MODE == kModeF16) {
+    // one activation per unrolled store loop: with the activation switch
+    // inside the loop, the accumulators ended up on the stack
+#define RG_CDS(ACTV) conv_direct_store_f16<ACTV, OMAX>(acc, bias, yb, L, O, act_param)
+    switch (act) {
+      case rgmath::ACT_RELU: RG_CDS(rgmath::ACT_RELU); break;
+      case rgmath::ACT_SIGMOID: RG_CDS(rgmath::ACT_SIGMOID); break;
+      case rgmath::ACT_TANH: RG_CDS(rgmath::ACT_TANH); break;
+      case rgmath::ACT_GELU: RG_CDS(rgmath::ACT_GELU); break;
+      case rgmath::ACT_LEAKY_RELU: RG_CDS(rgmath::ACT_LEAKY_RELU); break;
+      case rgmath::ACT_SILU: RG_CDS(rgmath::ACT_SILU); break;
+      default: RG_CDS(rgmath::ACT_NONE); break;
     }
-    yb[(int64_t)o * L] = v;
+#undef RG_CDS
+  } else {
+#pragma unroll
+    for (int o = 0; o < OMAX; o++)
+      if (o < O) yb[(int64_t)o * L] = acc[o] + bias[o];
   }
 }
 
