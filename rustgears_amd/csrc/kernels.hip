@@ -2045,6 +2045,66 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
   }
 }
 
+// Conv -> MaxPool2d(2, 2) (npu.rs:384-390 on the output of npu.rs:319-383)
+// in the conv's epilogue: only the pooled output is stored.  Host-checked
+// shape: OH, OW even, OW = 16 R16, and every wave's TN/4 pixels are whole
+// pairs of output rows, so fragment j of an even row (j / R16 even) has the
+// next row in fragment j + R16 of the same lane and pixel p + 1 in lane ^ 1.
+// An even lane takes its window in the reference's order (0,0), (0,1),
+// (1,0), (1,1) with pool_take from -inf (maxpool2_kernel's rule), and the
+// absmax for the next op is over the pooled values.
+__device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
+
+template <int TM, int TN, int ACT, int R16>
+__device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
+                                                         const Epilogue& ep, int b, int o0,
+                                                         const int (&pix)[TN / 64], float csc, int lane) {
+  constexpr int FM = TM / 16, FN = TN / 64;
+  static_assert(FN % (2 * R16) == 0, "a wave's pixels are whole pairs of output rows");
+  const int64_t O = cs.O;
+  const int OW = (int)cs.OW, L = (int)(cs.OH * cs.OW), POW = OW >> 1;
+  const int64_t PL = (int64_t)(cs.OH >> 1) * POW;
+  const bool even = (lane & 1) == 0;
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int o = o0 + i * 16 + (lane >> 4) * 4 + r;
+      const float bias = ep.bias[o];  // padded to Opad
+      float v[FN], h[FN];
+#pragma unroll
+      for (int j = 0; j < FN; j++) v[j] = epi_value<ACT>(acc[i][j][r], csc, bias, ep.act_param);
+#pragma unroll
+      for (int j = 0; j < FN; j++) h[j] = __shfl_xor(v[j], 1);
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        if ((j / R16) % 2 != 0) continue;
+        const int jn = j + R16 < FN ? j + R16 : j;  // j + R16 whenever j's row is even
+        float best = -__builtin_inff();
+        best = pool_take(best, v[j]);
+        best = pool_take(best, h[j]);
+        best = pool_take(best, v[jn]);
+        best = pool_take(best, h[jn]);
+        const int p = pix[j];
+        if (even && o < O && p < L) {
+          const int oy = p / OW, ox = p - oy * OW;
+          ep.y[((int64_t)b * O + o) * PL + (oy >> 1) * POW + (ox >> 1)] = best;
+          const uint32_t key = rgmath::absmax_key(best);
+          amax = key > amax ? key : amax;
+        }
+      }
+    }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (ep.absmax_out_per_image) {
+      if (lane == 0 && amax) atomicMax(ep.absmax_out + b, amax);
+    } else if (lane == 0) {
+      spread_max(ep.absmax_out, amax);
+    }
+  }
+}
+
 constexpr int64_t kConvSelfAbsmaxMax = 16384;
 
 // Publishes a block-measured per-image absmax in the image's slot (zeroed
@@ -2231,6 +2291,22 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
     csc = img_scale * ep.w_scale;
   else
     csc = slot_scale(ep.absmax_in + b) * ep.w_scale;
+  if constexpr (XF && TN / 64 >= 2) {
+    // the fused 2 x 2 pool (ReLU or no activation; try_conv_band checks the shape)
+    if (ep.pool2) {
+      const bool relu = ep.act == rgmath::ACT_RELU;
+      if constexpr (TN / 64 >= 4) {
+        if (ep.pool2 == 2) {
+          relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 2>(acc, cs, ep, b, o0, pix, csc, lane)
+               : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 2>(acc, cs, ep, b, o0, pix, csc, lane);
+          return;
+        }
+      }
+      relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 1>(acc, cs, ep, b, o0, pix, csc, lane)
+           : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 1>(acc, cs, ep, b, o0, pix, csc, lane);
+      return;
+    }
+  }
   switch (ep.act) {
     case rgmath::ACT_RELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_RELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
     case rgmath::ACT_SIGMOID: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SIGMOID>(acc, cs, ep, b, o0, pix, csc, lane); break;
@@ -2337,6 +2413,8 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
 template <int TM, int TN, bool CP4, bool XF>
 static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
                           int self_absmax = 0, SlotClear clear = SlotClear{}) {
+  // the fused pool needs whole pairs of output rows per wave (TN / 4 pixels)
+  if (ep.pool2 && (!XF || (TN / 4) % (32 * ep.pool2) != 0)) return false;
   const ConvBand g = conv_band_geom(cs, TM, TN);
   constexpr int kStatic = XF ? 64 : 0;  // the f32 form's few words of static LDS
   constexpr int kMaxLds = 160 * 1024 - kStatic;
@@ -2364,6 +2442,16 @@ static bool try_conv_band_tn(const int8_t* xq, const int8_t* Wq, const ConvShape
 
 bool conv_self_absmax_supported(const ConvShape& cs) { return cs.C * cs.H * cs.W <= kConvSelfAbsmaxMax; }
 
+bool conv_pool_supported(const ConvShape& cs, int r16) {
+  if (r16 != 1 && r16 != 2) return false;
+  if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31)) return false;
+  const int TM = cs.Opad % 64 == 0 ? 64 : 32;
+  constexpr int kMaxLds = 160 * 1024 - 64;  // try_conv_band's bound for the f32-input form
+  for (const int TN : {256, 128})
+    if ((TN / 4) % (32 * r16) == 0 && conv_band_geom(cs, TM, TN).lds_bytes <= kMaxLds) return true;
+  return false;
+}
+
 bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
                        bool self_absmax, SlotClear clear) {
   if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31))
@@ -2380,6 +2468,7 @@ bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, co
 }
 
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {
+  if (ep.pool2) throw std::logic_error("conv: the fused pool needs the f32-input conv");
   if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31))
     throw std::logic_error("conv: shape too large for the kernel's indexing");
   const bool cp4 = cs.cp == 4;
@@ -2463,8 +2552,6 @@ __global__ __launch_bounds__(256) void maxpool_kernel(const float* __restrict__ 
 // raising neighbouring slots serialise at the memory side.  Each output takes
 // its window in the reference's order (0,0), (0,1), (1,0), (1,1) with the
 // same rule as maxpool_kernel, so ties and NaNs resolve alike.
-__device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
-
 constexpr int kPool2Threads = 1024, kPool2PerThread = 4;
 
 __global__ __launch_bounds__(kPool2Threads) void maxpool2_kernel(const float* __restrict__ x, float* __restrict__ y,

@@ -150,10 +150,16 @@ struct OpPlan {
   // FP16 Linear -> FP16 Linear: the producer's GEMM epilogue writes the
   // consumer's binary16 operand (q_ready / q_in of the consumer as above).
   bool handoff = false;
+  // INT8 conv -> MaxPool2d(2, 2) in the conv's epilogue: pool_r16 (OW / 16)
+  // on the conv, which writes the pooled output to its out_buf; pool_fused
+  // on the pool, which launches nothing and passes that buffer on.
+  int pool_r16 = 0;
+  bool pool_fused = false;
 };
 
 struct Plan {
   std::vector<int64_t> in_shape, out_shape;
+  bool capture = false;  // made for capture runs (no conv-pool fusion)
   int64_t in_len = 0, out_len = 0;
   std::vector<OpPlan> ops;
   size_t f32_elems = 0, q_bytes = 0, ylo_elems = 0;
@@ -624,6 +630,23 @@ static int64_t numel(const std::vector<int64_t>& s) {
 
 // With `scratch` the plan's buffers are views into that device array (of
 // kScratchBytes) instead of allocations of their own.
+// INT8 conv i followed by MaxPool2d(2, 2) that the conv's epilogue can do
+// (conv_band_epilogue_pool2): ReLU or no activation, even output height and
+// width of 16 or 32, no capture (which keeps the conv's own output).
+// Returns OW / 16, or 0.  RGNPU_CONV_POOL=0 turns the fusion off.
+static int conv_pool_fusion(const rgnpu_program* P, const std::vector<OpPlan>& plan_ops, size_t i) {
+  const char* e = getenv("RGNPU_CONV_POOL");
+  if ((e && atoi(e) == 0) || P->capture || P->precision != RGNPU_PRECISION_INT8 || i + 1 >= P->ops.size()) return 0;
+  const Op& op = *P->ops[i];
+  const Op& pool = *P->ops[i + 1];
+  if (op.kind != OP_CONV || pool.kind != OP_POOL || pool.k != 2 || pool.s != 2) return 0;
+  if (op.act != rgmath::ACT_NONE && op.act != rgmath::ACT_RELU) return 0;
+  const ConvShape& c = plan_ops[i].cs;
+  if (c.OH % 2 != 0 || (c.OW != 16 && c.OW != 32) || c.n <= 0) return 0;
+  const int r16 = (int)(c.OW / 16);
+  return conv_pool_supported(c, r16) ? r16 : 0;
+}
+
 static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, int ndim, void* scratch = nullptr) {
   if (ndim < 1 || ndim > 8) throw Error(RGNPU_ERR_SHAPE, "input rank must be 1..8");
   auto plan = std::make_unique<Plan>();
@@ -703,14 +726,19 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
 
   // Buffers: f32 ping-pong between ops, the last computing op writes the
   // caller's output.
+  plan->capture = P->capture;
+  for (size_t i = 0; i + 1 < nops; i++) {
+    plan->ops[i].pool_r16 = conv_pool_fusion(P, plan->ops, i);
+    plan->ops[i + 1].pool_fused = plan->ops[i].pool_r16 != 0;
+  }
   int last = -1;
   for (size_t i = 0; i < nops; i++)
-    if (P->ops[i]->kind != OP_FLATTEN) last = (int)i;
+    if (P->ops[i]->kind != OP_FLATTEN && !plan->ops[i].pool_fused) last = (int)i;
   int curbuf = BUF_INPUT;
   for (size_t i = 0; i < nops; i++) {
     OpPlan& pl = plan->ops[i];
     pl.in_buf = curbuf;
-    if (P->ops[i]->kind == OP_FLATTEN) {
+    if (P->ops[i]->kind == OP_FLATTEN || pl.pool_fused) {
       pl.out_buf = curbuf;
     } else if ((int)i == last) {
       pl.out_buf = BUF_OUTPUT;
@@ -927,7 +955,7 @@ static void ensure_capture_buffers(rgnpu_program* P, Plan& plan) {
 static void finalize_profile(rgnpu_program* P);
 
 static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
-  if (P->plan && (int)P->plan->in_shape.size() == ndim &&
+  if (P->plan && (int)P->plan->in_shape.size() == ndim && P->plan->capture == P->capture &&
       std::equal(P->plan->in_shape.begin(), P->plan->in_shape.end(), shape))
     return *P->plan;
   // A pending profile reads the roles and events of the plan it ran with:
@@ -1218,6 +1246,15 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         ep.absmax_out = emit;
         ep.absmax_out_per_image = pl.emit_per_image;
         ep.acc_out = cap ? plan.cap_acc[i]->as<int32_t>() : nullptr;
+        // Conv -> MaxPool2d(2, 2): the conv's epilogue pools, stores only the
+        // pool's output (in this op's out buffer) and raises its absmax for
+        // the next op; the pool op then launches nothing.
+        if (pl.pool_r16) {
+          const OpPlan& ppl = plan.ops[i + 1];
+          ep.pool2 = pl.pool_r16;
+          ep.absmax_out = ppl.emit_slot >= 0 ? slots + ppl.emit_slot : nullptr;
+          ep.absmax_out_per_image = ppl.emit_per_image;
+        }
         // The conv quantizes the f32 image into its LDS band itself; the
         // separate i8 image is made only for the capture tap (after the conv
         // when the conv measures the absmax), or when the band does not fit
@@ -1227,6 +1264,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         bool fused = false;
         if (c.n > 0 && c.OH * c.OW > 0) {
           fused = launch_conv_f32in(in, op.d_w.as<int8_t>(), c, ep, s, self_absmax, clear);
+          if (ep.pool2 && !fused) throw std::logic_error("conv with pool: no tile width fits (plan said one does)");
           if (self_absmax && fused) first_launched();
           if (!fused) {
             if (self_absmax) {  // the band does not fit: the absmax pass after all
@@ -1248,6 +1286,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
       case OP_POOL: {
         const auto& is = pl.in_shape;
         pre = launch_events_used();
+        if (pl.pool_fused) break;  // done in the conv's epilogue
         launch_maxpool(in, out, is[0], is[1], is[2], is[3], op.k, op.s, pl.out_shape[2], pl.out_shape[3], emit,
                        pl.emit_per_image, s);
         break;

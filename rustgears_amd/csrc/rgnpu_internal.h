@@ -54,6 +54,9 @@ struct Epilogue {
   uint16_t* h_out = nullptr;
   int64_t ldh = 0;
   int gelu_cert = 0;  // with h_out and GELU: 1 certified (2, 3 test modes as in Requant), 0 exact
+  // INT8 conv -> MaxPool2d(2, 2): y is the pool's output [n, O, OH/2, OW/2]
+  // and absmax_out its absmax; the value is OW / 16 (1 or 2), 0 = no pool.
+  int pool2 = 0;
 };
 
 // Requantization fused into a producing Linear's GEMM (requant.hip): the
@@ -213,8 +216,14 @@ void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const 
 // band does not fit in LDS (then quantize the image and use launch_conv).
 // With self_absmax (conv_self_absmax_supported: small, fully covered
 // images) the kernel measures each image's absmax itself, publishes it in
-// ep.absmax_in, and zeroes `clear` (the run's first kernel).
+// ep.absmax_in, and zeroes `clear` (the run's first kernel).  With
+// ep.pool2 (see Epilogue) it also returns false when no tile width fits
+// the pool; then launch it without.
 bool conv_self_absmax_supported(const ConvShape& cs);
+// Whether launch_conv_f32in can pool 2 x 2 in its epilogue (ep.pool2 = r16 =
+// OW / 16): some tile width it tries holds whole pairs of output rows per
+// wave and fits in LDS.
+bool conv_pool_supported(const ConvShape& cs, int r16);
 bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
                        bool self_absmax = false, SlotClear clear = SlotClear{});
 
