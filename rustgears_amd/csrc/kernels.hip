@@ -1065,26 +1065,44 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_big_kernel(
 template <int ACT, int MODE>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const int32_t* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, int64_t Mpad, int64_t Npad, Epilogue ep) {
-  float cs = 1.0f;
-  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   const int64_t n4 = Npad / 4, total = M * n4;
   uint32_t amax = 0;
+  float cs = 1.0f;
+  if constexpr (MODE == kModeI8) cs = tensor_scale(ep.absmax_in) * ep.w_scale;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / n4, c0 = (e - row * n4) * 4;
+    const v4f bias = *reinterpret_cast<const v4f*>(ep.bias + c0);  // padded to Npad
+    // The partials are loaded KB at a time, all issued before any is added
+    // (a load-add loop waits for each in turn), then added in slice order;
+    // past S a lane re-reads the last partial and does not add it.
+    constexpr int KB = 8;
     v4i sum = v4i{0, 0, 0, 0};
-    if constexpr (MODE != kModeI8) {
-      v4f f = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int sp = 0; sp < S; sp++)
-        f += __builtin_bit_cast(v4f, *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0));
-      sum = __builtin_bit_cast(v4i, f);
-    } else {
-      for (int sp = 0; sp < S; sp++) sum += *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0);
+    v4f f = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sp0 = 0; sp0 < S; sp0 += KB) {
+      v4i part[KB];
+#pragma unroll
+      for (int u = 0; u < KB; u++) {
+        const int sp = sp0 + u < S ? sp0 + u : S - 1;
+        part[u] = *reinterpret_cast<const v4i*>(ws + ((int64_t)sp * Mpad + row) * Npad + c0);
+      }
+#pragma unroll
+      for (int u = 0; u < KB; u++) {
+        const bool ok = sp0 + u < S;  // a select, not a branch, so no load waits alone
+        if constexpr (MODE != kModeI8) {
+          const v4f g = f + __builtin_bit_cast(v4f, part[u]);
+          f = ok ? g : f;
+        } else {
+          const v4i g = sum + part[u];
+          sum = ok ? g : sum;
+        }
+      }
     }
+    if constexpr (MODE != kModeI8) sum = __builtin_bit_cast(v4i, f);
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int64_t col = c0 + q;
       if (col < N) {
-        const float v = epi_word<ACT, MODE>(sum[q], cs, ep.bias[col], ep.act_param);
+        const float v = epi_word<ACT, MODE>(sum[q], cs, bias[q], ep.act_param);
         ep.y[row * N + col] = v;
         if (ep.acc_out) ep.acc_out[row * N + col] = sum[q];
         const uint32_t k = rgmath::absmax_key(v);
