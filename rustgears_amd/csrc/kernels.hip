@@ -441,10 +441,46 @@ __device__ __forceinline__ void conv_direct_store_f16(const float (&acc)[OMAX], 
     if (o < O) yb[(int64_t)o * L] = act_fixed<ACT>(rgmath::round_fp16(acc[o] + bias[o]), act_param);
 }
 
+// The max pool's window step: NaN propagates and ties keep the earlier
+// element (kernels.rs:180-191).
+__device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
+
+// FP16 direct conv -> MaxPool2d(2, 2) (npu.rs:384-390): the outputs as in
+// conv_direct_store_f16, pooled in registers.  OW is 16 or 32 and OH even
+// (host-checked), so a wave's 64 pixels are whole pairs of output rows:
+// pixel p + 1 is in lane ^ 1 and p + OW in lane ^ OW.  The even-row,
+// even-column lanes take the window in the reference's order with
+// pool_take and store the pooled value; every lane takes part in the
+// shuffles (lanes past the last pixel computed a clamped one).
+template <int ACT, int OMAX>
+__device__ __forceinline__ void conv_direct_pool_f16(const float (&acc)[OMAX], const float* __restrict__ bias,
+                                                     float* __restrict__ y, int64_t b, int O, int OH, int OW,
+                                                     int64_t pix, bool live, float act_param) {
+  const int oy = (int)(pix / OW), ox = (int)(pix - (int64_t)oy * OW);
+  const bool lead = live && (oy & 1) == 0 && (ox & 1) == 0;
+  const int64_t PL = (int64_t)(OH >> 1) * (OW >> 1);
+  float* const yb = y + b * (int64_t)O * PL + (oy >> 1) * (OW >> 1) + (ox >> 1);
+#pragma unroll
+  for (int o = 0; o < OMAX; o++) {
+    if (o < O) {  // O is the same for the whole wave (no break: it put acc on the stack)
+      const float v = act_fixed<ACT>(rgmath::round_fp16(acc[o] + bias[o]), act_param);
+      const float h = __shfl_xor(v, 1);
+      const float d = __shfl_xor(v, OW);
+      const float dh = __shfl_xor(h, OW);
+      float best = -__builtin_inff();
+      best = pool_take(best, v);
+      best = pool_take(best, h);
+      best = pool_take(best, d);
+      best = pool_take(best, dh);
+      if (lead) yb[(int64_t)o * PL] = best;
+    }
+  }
+}
+
 template <int OMAX, int MODE>
 __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restrict__ x, const void* __restrict__ wv,
                                                           const float* __restrict__ bias, float* __restrict__ y,
-                                                          ConvShape cs, int act, float act_param) {
+                                                          ConvShape cs, int act, float act_param, int pool2) {
   // weights as f32, tap-major [tap][OMAX] (channels past O are zero), so a
   // tap's weights are OMAX / 4 broadcast 16-byte LDS reads
   __shared__ __attribute__((aligned(16))) float ws[kDirectConvTaps * OMAX];
@@ -463,8 +499,10 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restric
   __syncthreads();
   const int64_t b = blockIdx.y;
   const int64_t L = cs.OH * cs.OW;
-  const int64_t pix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (pix >= L) return;
+  const int64_t pix_raw = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool live = pix_raw < L;
+  if (!live && !pool2) return;
+  const int64_t pix = live ? pix_raw : L - 1;  // pooled: every lane joins the shuffles
   const int oy = (int)(pix / cs.OW), ox = (int)(pix - (int64_t)oy * cs.OW);
   const int iy0 = oy * (int)cs.stride - (int)cs.pad, ix0 = ox * (int)cs.stride - (int)cs.pad;
   const int H = (int)cs.H, W = (int)cs.W;
@@ -507,6 +545,13 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restric
     }
   float* yb = y + b * (int64_t)O * L + pix;
   if constexpr (MODE == kModeF16) {
+    if (pool2) {
+      if (act == rgmath::ACT_RELU)
+        conv_direct_pool_f16<rgmath::ACT_RELU, OMAX>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
+      else
+        conv_direct_pool_f16<rgmath::ACT_NONE, OMAX>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
+      return;
+    }
     // one activation per unrolled store loop: with the activation switch
     // inside the loop, the accumulators ended up on the stack
 #define RG_CDS(ACTV) conv_direct_store_f16<ACTV, OMAX>(acc, bias, yb, L, O, act_param)
@@ -529,29 +574,32 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restric
 
 template <int MODE>
 static void launch_conv_direct_t(const float* x, const void* w, const float* bias, float* y, const ConvShape& cs,
-                                 int act, float act_param, hipStream_t s) {
+                                 int act, float act_param, int pool2, hipStream_t s) {
   if (cs.C * cs.k * cs.k > kDirectConvTaps || cs.O > 64 || cs.O <= 0)
     throw std::logic_error("direct conv: window or output channels too large");
+  if (pool2 && (MODE != kModeF16 || (pool2 != 16 && pool2 != 32) || cs.OW != pool2 || cs.OH % 2 != 0 ||
+                (act != rgmath::ACT_RELU && act != rgmath::ACT_NONE)))
+    throw std::logic_error("direct conv: the fused pool needs FP16, ReLU or none, even height, width 16 or 32");
   const int64_t L = cs.OH * cs.OW;
   if (L <= 0 || cs.n <= 0) return;
   if (cs.n > 65535) throw std::logic_error("direct conv: too many images for one launch");
   const dim3 grid((unsigned)((L + 255) / 256), (unsigned)cs.n);
   if (cs.O <= 16)
-    RG_LAUNCH((conv_direct_kernel<16, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+    RG_LAUNCH((conv_direct_kernel<16, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param, pool2);
   else if (cs.O <= 32)
-    RG_LAUNCH((conv_direct_kernel<32, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+    RG_LAUNCH((conv_direct_kernel<32, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param, pool2);
   else
-    RG_LAUNCH((conv_direct_kernel<64, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param);
+    RG_LAUNCH((conv_direct_kernel<64, MODE>), grid, dim3(256), 0, s, x, w, bias, y, cs, act, act_param, pool2);
 }
 
 void launch_conv_direct_f16(const float* x, const uint16_t* w, const float* bias, float* y, const ConvShape& cs,
-                            int act, float act_param, hipStream_t s) {
-  launch_conv_direct_t<kModeF16>(x, w, bias, y, cs, act, act_param, s);
+                            int act, float act_param, int pool_ow, hipStream_t s) {
+  launch_conv_direct_t<kModeF16>(x, w, bias, y, cs, act, act_param, pool_ow, s);
 }
 
 void launch_conv_direct_f32(const float* x, const float* w, const float* bias, float* y, const ConvShape& cs,
                             hipStream_t s) {
-  launch_conv_direct_t<kModeF32>(x, w, bias, y, cs, rgmath::ACT_NONE, 0.0f, s);
+  launch_conv_direct_t<kModeF32>(x, w, bias, y, cs, rgmath::ACT_NONE, 0.0f, 0, s);
 }
 
 void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s) {
@@ -2071,7 +2119,6 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
 // An even lane takes its window in the reference's order (0,0), (0,1),
 // (1,0), (1,1) with pool_take from -inf (maxpool2_kernel's rule), and the
 // absmax for the next op is over the pooled values.
-__device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
 
 template <int TM, int TN, int ACT, int R16>
 __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,

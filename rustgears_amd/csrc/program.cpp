@@ -630,13 +630,15 @@ static int64_t numel(const std::vector<int64_t>& s) {
 
 // With `scratch` the plan's buffers are views into that device array (of
 // kScratchBytes) instead of allocations of their own.
-// INT8 conv i followed by MaxPool2d(2, 2) that the conv's epilogue can do
-// (conv_band_epilogue_pool2): ReLU or no activation, even output height and
-// width of 16 or 32, no capture (which keeps the conv's own output).
-// Returns OW / 16, or 0.  RGNPU_CONV_POOL=0 turns the fusion off.
+// Conv i followed by MaxPool2d(2, 2) that the conv can do itself: ReLU or
+// no activation, even output height and width of 16 or 32, no capture
+// (which keeps the conv's own output); INT8 on the band kernel
+// (conv_band_epilogue_pool2, when a tile width fits), FP16 on the direct
+// conv (conv_direct_pool_f16).  Returns OW / 16, or 0.  RGNPU_CONV_POOL=0
+// turns the fusion off.
 static int conv_pool_fusion(const rgnpu_program* P, const std::vector<OpPlan>& plan_ops, size_t i) {
   const char* e = getenv("RGNPU_CONV_POOL");
-  if ((e && atoi(e) == 0) || P->capture || P->precision != RGNPU_PRECISION_INT8 || i + 1 >= P->ops.size()) return 0;
+  if ((e && atoi(e) == 0) || P->capture || P->precision == RGNPU_PRECISION_FP32 || i + 1 >= P->ops.size()) return 0;
   const Op& op = *P->ops[i];
   const Op& pool = *P->ops[i + 1];
   if (op.kind != OP_CONV || pool.kind != OP_POOL || pool.k != 2 || pool.s != 2) return 0;
@@ -644,6 +646,8 @@ static int conv_pool_fusion(const rgnpu_program* P, const std::vector<OpPlan>& p
   const ConvShape& c = plan_ops[i].cs;
   if (c.OH % 2 != 0 || (c.OW != 16 && c.OW != 32) || c.n <= 0) return 0;
   const int r16 = (int)(c.OW / 16);
+  if (P->precision == RGNPU_PRECISION_FP16)  // the direct conv, as enqueue picks it
+    return plan_ops[i].rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64 ? r16 : 0;
   return conv_pool_supported(c, r16) ? r16 : 0;
 }
 
@@ -1207,7 +1211,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         if (f16) {  // npu.rs:341-376: im2col, GEMM, transpose per image
           pre = launch_events_used();
           if (pl.rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64) {
-            launch_conv_direct_f16(in, op.d_w.as<uint16_t>(), op.d_bias.as<float>(), out, c, op.act, op.act_param, s);
+            launch_conv_direct_f16(in, op.d_w.as<uint16_t>(), op.d_bias.as<float>(), out, c, op.act, op.act_param,
+                                   pl.pool_r16 ? (int)c.OW : 0, s);
           } else if (pl.rows > 0) {
             uint16_t* h = plan.q.as<uint16_t>();
             launch_im2col_half(in, c, pl.Mpad, op.Kpad, h, s);

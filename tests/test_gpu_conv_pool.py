@@ -13,6 +13,10 @@ The profile keeps the pool's record. A fused pool launches nothing.
 
 Shapes the fusion does not take are checked too: width 24 or 64, odd height,
 pool window 3, and sigmoid.  These run the conv and then the pool kernel.
+
+The FP16 direct conv (kernels.hip conv_direct_pool_f16) pools the same way.
+Its fused output must equal the unfused one bit for bit, and the unfused
+FP16 path is checked against the oracle in test_gpu_fp16.py.
 """
 import numpy as np
 import pytest
@@ -22,11 +26,12 @@ from conftest import assert_bitexact_f32
 pytestmark = pytest.mark.gpu
 
 
-def _run(rg, layers, x, fusion):
+def _run(rg, layers, x, fusion, fp16=False):
     import os
     os.environ["RGNPU_CONV_POOL"] = "1" if fusion else "0"
     try:
-        sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+        ep = rg.ExecutionProvider.mi355x_fp16() if fp16 else rg.ExecutionProvider.mi355x_int8()
+        sess = rg.InferenceSession.from_layers(layers, ep)
         y = sess.run(x)
         y2 = sess.run(x)
         prof = sess.last_npu_profile()
@@ -140,3 +145,37 @@ def test_capture_turns_the_fusion_off(rg, ref):
     assert_bitexact_f32(y, want, "fused again")
     assert [r.kernel_ns == 0 for r in sess.last_npu_profile().records if "MaxPool" in r.op] == [True, True]
     sess.close()
+
+
+FP16_CASES = [
+    # (name, c, o, (h, w), act, tail, images, fused)
+    ("bench CNN's first conv", 3, 32, (32, 32), "relu", "conv", 4, True),
+    ("width 16, 64 channels, no activation", 3, 64, (16, 16), None, "linear", 3, True),
+    ("ragged last wave (L = 16 x 6)", 2, 16, (6, 16), "relu", None, 5, True),
+    ("odd height: not fused", 3, 32, (15, 16), "relu", "linear", 2, False),
+    ("width 64: not fused", 3, 32, (8, 64), "relu", "linear", 2, False),
+]
+
+
+@pytest.mark.parametrize("name,c,o,hw,act,tail,n,fused", FP16_CASES, ids=[c[0] for c in FP16_CASES])
+def test_fp16_direct_conv_pool(rg, name, c, o, hw, act, tail, n, fused):
+    layers = _conv_pool_model(rg, 500 + c + o, c, o, hw, act, tail)
+    x = rg.randn([n, c, hw[0], hw[1]])
+    print(f"[conv-pool fp16] {name} x{tuple(x.shape)}", flush=True)
+    y, prof = _run(rg, layers, x, True, fp16=True)
+    y0, prof0 = _run(rg, layers, x, False, fp16=True)
+    assert_bitexact_f32(y, y0, name)
+    pools = [r for r in prof.records if r.op.startswith("NPU::MaxPool2d")]
+    assert [r.kernel_ns == 0 for r in pools][:1] == [fused], (name, pools)
+    assert all(r.kernel_ns > 0 for r in prof0.records if r.op.startswith("NPU::MaxPool2d"))
+
+
+def test_fp16_special_values_through_the_fused_pool(rg):
+    layers = _conv_pool_model(rg, 91, 3, 32, (16, 32), None, None)
+    conv = layers[0]
+    conv.bias[[1, 9]] = np.float32(np.nan)
+    conv.bias[[4, 20]] = np.float32(-np.inf)
+    x = rg.randn([3, 3, 16, 32])
+    y, _ = _run(rg, layers, x, True, fp16=True)
+    y0, _ = _run(rg, layers, x, False, fp16=True)
+    assert_bitexact_f32(y, y0, "fp16 special values")
