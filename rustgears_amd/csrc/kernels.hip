@@ -445,15 +445,16 @@ __device__ __forceinline__ void conv_direct_store_f16(const float (&acc)[OMAX], 
 // element (kernels.rs:180-191).
 __device__ __forceinline__ float pool_take(float best, float v) { return (v > best || v != v) ? v : best; }
 
-// FP16 direct conv -> MaxPool2d(2, 2) (npu.rs:384-390): the outputs as in
-// conv_direct_store_f16, pooled in registers.  OW is 16 or 32 and OH even
+// Direct conv -> MaxPool2d(2, 2) (npu.rs:384-390): the outputs as in
+// conv_direct_store_f16 (FP16) or the FP32 store followed by the
+// activation op's act_fixed (FP32: conv, Act, pool), pooled in registers.  OW is 16 or 32 and OH even
 // (host-checked), so a wave's 64 pixels are whole pairs of output rows:
 // pixel p + 1 is in lane ^ 1 and p + OW in lane ^ OW.  The even-row,
 // even-column lanes take the window in the reference's order with
 // pool_take and store the pooled value; every lane takes part in the
 // shuffles (lanes past the last pixel computed a clamped one).
-template <int ACT, int OMAX>
-__device__ __forceinline__ void conv_direct_pool_f16(const float (&acc)[OMAX], const float* __restrict__ bias,
+template <int ACT, int OMAX, int MODE>
+__device__ __forceinline__ void conv_direct_pool(const float (&acc)[OMAX], const float* __restrict__ bias,
                                                      float* __restrict__ y, int64_t b, int O, int OH, int OW,
                                                      int64_t pix, bool live, float act_param) {
   const int oy = (int)(pix / OW), ox = (int)(pix - (int64_t)oy * OW);
@@ -463,7 +464,8 @@ __device__ __forceinline__ void conv_direct_pool_f16(const float (&acc)[OMAX], c
 #pragma unroll
   for (int o = 0; o < OMAX; o++) {
     if (o < O) {  // O is the same for the whole wave (no break: it put acc on the stack)
-      const float v = act_fixed<ACT>(rgmath::round_fp16(acc[o] + bias[o]), act_param);
+      const float s = acc[o] + bias[o];
+      const float v = act_fixed<ACT>(MODE == kModeF16 ? rgmath::round_fp16(s) : s, act_param);
       const float h = __shfl_xor(v, 1);
       const float d = __shfl_xor(v, OW);
       const float dh = __shfl_xor(h, OW);
@@ -543,15 +545,15 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(const float* __restric
         }
       }
     }
+  if (pool2) {
+    if (act == rgmath::ACT_RELU)
+      conv_direct_pool<rgmath::ACT_RELU, OMAX, MODE>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
+    else
+      conv_direct_pool<rgmath::ACT_NONE, OMAX, MODE>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
+    return;
+  }
   float* yb = y + b * (int64_t)O * L + pix;
   if constexpr (MODE == kModeF16) {
-    if (pool2) {
-      if (act == rgmath::ACT_RELU)
-        conv_direct_pool_f16<rgmath::ACT_RELU, OMAX>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
-      else
-        conv_direct_pool_f16<rgmath::ACT_NONE, OMAX>(acc, bias, y, b, O, (int)cs.OH, (int)cs.OW, pix, live, act_param);
-      return;
-    }
     // one activation per unrolled store loop: with the activation switch
     // inside the loop, the accumulators ended up on the stack
 #define RG_CDS(ACTV) conv_direct_store_f16<ACTV, OMAX>(acc, bias, yb, L, O, act_param)
@@ -577,9 +579,9 @@ static void launch_conv_direct_t(const float* x, const void* w, const float* bia
                                  int act, float act_param, int pool2, hipStream_t s) {
   if (cs.C * cs.k * cs.k > kDirectConvTaps || cs.O > 64 || cs.O <= 0)
     throw std::logic_error("direct conv: window or output channels too large");
-  if (pool2 && (MODE != kModeF16 || (pool2 != 16 && pool2 != 32) || cs.OW != pool2 || cs.OH % 2 != 0 ||
+  if (pool2 && ((pool2 != 16 && pool2 != 32) || cs.OW != pool2 || cs.OH % 2 != 0 ||
                 (act != rgmath::ACT_RELU && act != rgmath::ACT_NONE)))
-    throw std::logic_error("direct conv: the fused pool needs FP16, ReLU or none, even height, width 16 or 32");
+    throw std::logic_error("direct conv: the fused pool needs ReLU or none, even height, width 16 or 32");
   const int64_t L = cs.OH * cs.OW;
   if (L <= 0 || cs.n <= 0) return;
   if (cs.n > 65535) throw std::logic_error("direct conv: too many images for one launch");
@@ -598,8 +600,8 @@ void launch_conv_direct_f16(const float* x, const uint16_t* w, const float* bias
 }
 
 void launch_conv_direct_f32(const float* x, const float* w, const float* bias, float* y, const ConvShape& cs,
-                            hipStream_t s) {
-  launch_conv_direct_t<kModeF32>(x, w, bias, y, cs, rgmath::ACT_NONE, 0.0f, 0, s);
+                            int pool_act, int pool_ow, hipStream_t s) {
+  launch_conv_direct_t<kModeF32>(x, w, bias, y, cs, pool_ow ? pool_act : rgmath::ACT_NONE, 0.0f, pool_ow, s);
 }
 
 void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s) {

@@ -150,10 +150,12 @@ struct OpPlan {
   // FP16 Linear -> FP16 Linear: the producer's GEMM epilogue writes the
   // consumer's binary16 operand (q_ready / q_in of the consumer as above).
   bool handoff = false;
-  // INT8 conv -> MaxPool2d(2, 2) in the conv's epilogue: pool_r16 (OW / 16)
-  // on the conv, which writes the pooled output to its out_buf; pool_fused
-  // on the pool, which launches nothing and passes that buffer on.
+  // Conv -> MaxPool2d(2, 2) in the conv (FP32: conv -> Act -> pool):
+  // pool_r16 (OW / 16) on the conv, which writes the pooled output to its
+  // out_buf; pool_fused on the ops it absorbs, which launch nothing and pass
+  // that buffer on.
   int pool_r16 = 0;
+  int pool_act = 0;  // FP32: the activation of the Act op it absorbs
   bool pool_fused = false;
 };
 
@@ -628,28 +630,41 @@ static int64_t numel(const std::vector<int64_t>& s) {
   return n;
 }
 
-// With `scratch` the plan's buffers are views into that device array (of
-// kScratchBytes) instead of allocations of their own.
 // Conv i followed by MaxPool2d(2, 2) that the conv can do itself: ReLU or
 // no activation, even output height and width of 16 or 32, no capture
 // (which keeps the conv's own output); INT8 on the band kernel
-// (conv_band_epilogue_pool2, when a tile width fits), FP16 on the direct
-// conv (conv_direct_pool_f16).  Returns OW / 16, or 0.  RGNPU_CONV_POOL=0
-// turns the fusion off.
-static int conv_pool_fusion(const rgnpu_program* P, const std::vector<OpPlan>& plan_ops, size_t i) {
+// (conv_band_epilogue_pool2, when a tile width fits), FP16 and FP32 on the
+// direct conv (conv_direct_pool).  FP32 convs carry no activation: there
+// the pattern is conv, Act (ReLU or none), pool.  Returns OW / 16, or 0,
+// with *span the number of ops after the conv that it absorbs and *act the
+// activation it applies.  RGNPU_CONV_POOL=0 turns the fusion off.
+static int conv_pool_fusion(const rgnpu_program* P, const std::vector<OpPlan>& plan_ops, size_t i, int* span,
+                            int* act) {
   const char* e = getenv("RGNPU_CONV_POOL");
-  if ((e && atoi(e) == 0) || P->capture || P->precision == RGNPU_PRECISION_FP32 || i + 1 >= P->ops.size()) return 0;
+  const bool f32 = P->precision == RGNPU_PRECISION_FP32;
+  const size_t n = f32 ? 2 : 1;
+  if ((e && atoi(e) == 0) || P->capture || i + n >= P->ops.size()) return 0;
   const Op& op = *P->ops[i];
-  const Op& pool = *P->ops[i + 1];
+  const Op& pool = *P->ops[i + n];
   if (op.kind != OP_CONV || pool.kind != OP_POOL || pool.k != 2 || pool.s != 2) return 0;
-  if (op.act != rgmath::ACT_NONE && op.act != rgmath::ACT_RELU) return 0;
+  int a = op.act;
+  if (f32) {
+    if (P->ops[i + 1]->kind != OP_ACT) return 0;
+    a = P->ops[i + 1]->act;
+  }
+  if (a != rgmath::ACT_NONE && a != rgmath::ACT_RELU) return 0;
   const ConvShape& c = plan_ops[i].cs;
   if (c.OH % 2 != 0 || (c.OW != 16 && c.OW != 32) || c.n <= 0) return 0;
   const int r16 = (int)(c.OW / 16);
-  if (P->precision == RGNPU_PRECISION_FP16)  // the direct conv, as enqueue picks it
+  *span = (int)n;
+  *act = a;
+  if (P->precision != RGNPU_PRECISION_INT8)  // the direct conv, as enqueue picks it
     return plan_ops[i].rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64 ? r16 : 0;
   return conv_pool_supported(c, r16) ? r16 : 0;
 }
+
+// With `scratch` the plan's buffers are views into that device array (of
+// kScratchBytes) instead of allocations of their own.
 
 static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, int ndim, void* scratch = nullptr) {
   if (ndim < 1 || ndim > 8) throw Error(RGNPU_ERR_SHAPE, "input rank must be 1..8");
@@ -732,8 +747,11 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   // caller's output.
   plan->capture = P->capture;
   for (size_t i = 0; i + 1 < nops; i++) {
-    plan->ops[i].pool_r16 = conv_pool_fusion(P, plan->ops, i);
-    plan->ops[i + 1].pool_fused = plan->ops[i].pool_r16 != 0;
+    int span = 0, act = 0;
+    plan->ops[i].pool_r16 = conv_pool_fusion(P, plan->ops, i, &span, &act);
+    if (!plan->ops[i].pool_r16) continue;
+    plan->ops[i].pool_act = act;
+    for (int k = 1; k <= span; k++) plan->ops[i + k].pool_fused = true;
   }
   int last = -1;
   for (size_t i = 0; i < nops; i++)
@@ -1194,7 +1212,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         if (f32) {  // mod.rs:274-290: conv2d_forward (im2col + matmul), then the bias
           pre = launch_events_used();
           if (pl.rows > 0 && op.K <= kDirectConvTaps && op.out_f <= 64) {
-            launch_conv_direct_f32(in, op.d_w.as<float>(), op.d_bias.as<float>(), out, c, s);
+            launch_conv_direct_f32(in, op.d_w.as<float>(), op.d_bias.as<float>(), out, c, pl.pool_act,
+                                   pl.pool_r16 ? (int)c.OW : 0, s);
           } else if (pl.rows > 0) {
             float* a = plan.q.as<float>();
             launch_im2col_f32(in, c, pl.Mpad, op.Kpad, a, s);
@@ -1301,6 +1320,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         break;
       case OP_ACT:
         pre = launch_events_used();
+        if (pl.pool_fused) break;  // applied by the conv before its pool
         launch_activation(in, out, pl.in_len, op.act, op.act_param, emit, s);
         break;
       case OP_AFFINE: {

@@ -247,14 +247,16 @@ void launch_im2col_half(const float* x, const ConvShape& cs, int64_t Mpad, int64
 void launch_nlo_to_nchw(const float* ylo, int64_t n, int64_t O, int64_t L, float* y, hipStream_t s);
 // Direct convolution (FP16 / FP32) for windows of at most kDirectConvTaps
 // values and at most 64 output channels: taps summed serially in im2col
-// order; w is [O, Kpad] (binary16 or f32), y NCHW.  FP16 with pool_ow = OW
+// order; w is [O, Kpad] (binary16 or f32), y NCHW.  With pool_ow = OW
 // (16 or 32; OH even; ReLU or no activation): y is the output of the
-// MaxPool2d(2, 2) that follows, [n, O, OH/2, OW/2]; 0 = no pool.
+// MaxPool2d(2, 2) that follows, [n, O, OH/2, OW/2]; 0 = no pool.  FP32 has
+// no activation of its own: pool_act is that of the Act op between the conv
+// and the pool.
 constexpr int64_t kDirectConvTaps = 32;
 void launch_conv_direct_f16(const float* x, const uint16_t* w, const float* bias, float* y, const ConvShape& cs,
                             int act, float act_param, int pool_ow, hipStream_t s);
 void launch_conv_direct_f32(const float* x, const float* w, const float* bias, float* y, const ConvShape& cs,
-                            hipStream_t s);
+                            int pool_act, int pool_ow, hipStream_t s);
 // Lone ChannelAffine: y = round_fp16(fl(round_fp16(x) * scale[c]) + shift[c]), c = index % C.
 void launch_affine_f16(const float* x, int64_t n, int64_t C, const float* scale, const float* shift, float* y,
                        hipStream_t s);

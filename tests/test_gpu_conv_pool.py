@@ -14,9 +14,11 @@ The profile keeps the pool's record. A fused pool launches nothing.
 Shapes the fusion does not take are checked too: width 24 or 64, odd height,
 pool window 3, and sigmoid.  These run the conv and then the pool kernel.
 
-The FP16 direct conv (kernels.hip conv_direct_pool_f16) pools the same way.
-Its fused output must equal the unfused one bit for bit, and the unfused
-FP16 path is checked against the oracle in test_gpu_fp16.py.
+The FP16 and FP32 direct convs (kernels.hip conv_direct_pool) pool the same
+way.  FP32 convs carry no activation, so there the conv, its Act op and the
+pool become one kernel.  Their fused output must equal the unfused one bit
+for bit.  The unfused paths are checked against the oracle in
+test_gpu_fp16.py and test_gpu_fp32.py.
 """
 import numpy as np
 import pytest
@@ -26,11 +28,14 @@ from conftest import assert_bitexact_f32
 pytestmark = pytest.mark.gpu
 
 
-def _run(rg, layers, x, fusion, fp16=False):
+def _run(rg, layers, x, fusion, fp16=False, fp32=False):
     import os
     os.environ["RGNPU_CONV_POOL"] = "1" if fusion else "0"
     try:
-        ep = rg.ExecutionProvider.mi355x_fp16() if fp16 else rg.ExecutionProvider.mi355x_int8()
+        if fp32:
+            ep = rg.ExecutionProvider.Gpu(0)
+        else:
+            ep = rg.ExecutionProvider.mi355x_fp16() if fp16 else rg.ExecutionProvider.mi355x_int8()
         sess = rg.InferenceSession.from_layers(layers, ep)
         y = sess.run(x)
         y2 = sess.run(x)
@@ -179,3 +184,25 @@ def test_fp16_special_values_through_the_fused_pool(rg):
     y, _ = _run(rg, layers, x, True, fp16=True)
     y0, _ = _run(rg, layers, x, False, fp16=True)
     assert_bitexact_f32(y, y0, "fp16 special values")
+
+
+FP32_CASES = [
+    # (name, c, o, (h, w), act, tail, images, fused)
+    ("conv, ReLU, pool (bench CNN's first conv)", 3, 32, (32, 32), "relu", "conv", 4, True),
+    ("conv, pool: no Act op between", 3, 64, (16, 16), None, "linear", 3, False),
+    ("ragged last wave", 2, 16, (6, 16), "relu", None, 5, True),
+    ("sigmoid: not fused", 3, 32, (16, 16), "sigmoid", "linear", 2, False),
+]
+
+
+@pytest.mark.parametrize("name,c,o,hw,act,tail,n,fused", FP32_CASES, ids=[c[0] for c in FP32_CASES])
+def test_fp32_direct_conv_act_pool(rg, name, c, o, hw, act, tail, n, fused):
+    layers = _conv_pool_model(rg, 700 + c + o, c, o, hw, act, tail)
+    x = rg.randn([n, c, hw[0], hw[1]])
+    print(f"[conv-pool fp32] {name} x{tuple(x.shape)}", flush=True)
+    y, prof = _run(rg, layers, x, True, fp32=True)
+    y0, prof0 = _run(rg, layers, x, False, fp32=True)
+    assert_bitexact_f32(y, y0, name)
+    if prof is not None and prof.records:
+        pools = [r for r in prof.records if "MaxPool2d" in r.op]
+        assert [r.kernel_ns == 0 for r in pools][:1] == [fused], (name, pools)
