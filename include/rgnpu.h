@@ -60,16 +60,22 @@ enum { RGNPU_PRECISION_INT8 = 0, RGNPU_PRECISION_FP16 = 1, RGNPU_PRECISION_FP32 
 /* One LayerSpec.  Weight layouts are exactly as Module::export produces
  * them: Linear weight [in_features, out_features] row-major
  * (src/nn/layers.rs:74-81), Conv2d weight [out, in, k, k]
- * (src/nn/layers.rs:151-161).  Fields a kind does not use are ignored. */
+ * (src/nn/layers.rs:151-161).  Fields a kind does not use are ignored.
+ * The size fields are 64-bit so that every u32 an .rtim file holds reads
+ * back unchanged, as the reference's `usize` fields do (src/save.rs:233-255).
+ * A ChannelAffine's scale and shift carry their own lengths: the reference
+ * loads them as two independent vectors (src/save.rs:254) and indexes shift
+ * only below scale.len() (src/inference/mod.rs:236-237, 246, 302). */
 typedef struct rgnpu_layer {
   int32_t kind;
-  int32_t in_features, out_features;                           /* Linear */
-  int32_t in_channels, out_channels, kernel, stride, padding;  /* Conv2d */
-  int32_t pool_kernel, pool_stride;                            /* MaxPool2d */
   int32_t act; float act_param;                                /* Activation */
+  int64_t in_features, out_features;                           /* Linear */
+  int64_t in_channels, out_channels, kernel, stride, padding;  /* Conv2d */
+  int64_t pool_kernel, pool_stride;                            /* MaxPool2d */
   const float* weight; int64_t weight_len;
   const float* bias; int64_t bias_len;
-  const float* scale; const float* shift; int64_t affine_len;  /* ChannelAffine */
+  const float* scale; int64_t scale_len;                       /* ChannelAffine */
+  const float* shift; int64_t shift_len;
 } rgnpu_layer;
 
 typedef struct rgnpu_program rgnpu_program;
@@ -107,7 +113,10 @@ typedef struct rgnpu_profile {
  * whose round_fp16 value is +-65536 (inputs in [65520, 65536)) saturates to
  * +-65504, the largest binary16 value.  A Linear layer may have at most
  * 2^26 output features (RGNPU_ERR_INVALID above that; the reference has no
- * such limit). */
+ * such limit), and every size field at most 2^31 - 1.  A ChannelAffine whose
+ * shift is shorter than its scale gives RGNPU_ERR_INVALID (the reference
+ * indexes shift[c] for every channel and panics); a longer shift is used up
+ * to the scale's length, as the reference does. */
 int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t precision,
                          int32_t device, rgnpu_program** out);
 
@@ -199,14 +208,29 @@ int64_t rgnpu_program_op_label(const rgnpu_program* prog, int64_t i, char* buf, 
 int64_t rgnpu_program_op_weight(const rgnpu_program* prog, int64_t i, int8_t* dst, int64_t cap, float* scale);
 
 /* Capture taps for bit-exactness checks (no counterpart in the reference,
- * which fuses these values away, quantize.rs:109-111).  When enabled, the
- * next runs keep per op: the i8 activations the GEMM consumed (Linear
- * [rows,in]; Conv2d [n, L, C*k*k] = transposed im2col per image), the
- * activation scale(s) (1 or n f32), the i32 accumulators (Linear [rows,out];
- * Conv2d [n, L, out]) and the op's f32 output.  rgnpu_program_capture copies
- * up to cap_bytes into dst and returns the element count (dst may be NULL). */
+ * which fuses these values away, quantize.rs:109-111).
+ *  - RGNPU_CAPTURE_FULL: the next runs use the capture forms of the kernels
+ *    (every value stored) and keep per op: the i8 activations the GEMM
+ *    consumed (Linear [rows,in]; Conv2d [n, L, C*k*k] = transposed im2col
+ *    per image), the activation scale(s) (1 or n f32), the i32 accumulators
+ *    (Linear [rows,out]; Conv2d [n, L, out]) and the op's f32 output.
+ *  - RGNPU_CAPTURE_PRODUCTION: the next runs use the production plan and
+ *    kernels unchanged (fused requantization with the certified GELU,
+ *    conv + pool fusion, operand hand-offs); after each op its i8 operand,
+ *    absmax slot and f32 output are copied device to device where they exist
+ *    in memory: the i8 activations of a Linear whose operand buffer was
+ *    written (not for the GEMMs that quantize as they read, nor for convs,
+ *    which quantize into LDS), the scale(s) from the absmax the consumer
+ *    read, and the f32 output of ops that store theirs (not of a GEMM that
+ *    writes the next op's operand instead, nor of a conv that pools in its
+ *    epilogue: the MaxPool2d op then shows the pooled output).  The i32
+ *    accumulators are never available; what is not available reads as 0
+ *    elements.
+ * rgnpu_program_capture copies up to cap_bytes into dst and returns the
+ * element count (dst may be NULL). */
 enum { RGNPU_CAP_QACT = 0, RGNPU_CAP_SCALE = 1, RGNPU_CAP_ACC = 2, RGNPU_CAP_OUT = 3 };
-int rgnpu_program_set_capture(rgnpu_program* prog, int32_t on);
+enum { RGNPU_CAPTURE_OFF = 0, RGNPU_CAPTURE_FULL = 1, RGNPU_CAPTURE_PRODUCTION = 2 };
+int rgnpu_program_set_capture(rgnpu_program* prog, int32_t mode);
 int64_t rgnpu_program_capture(rgnpu_program* prog, int64_t op, int32_t what, void* dst, int64_t cap_bytes);
 
 void rgnpu_program_destroy(rgnpu_program* prog);

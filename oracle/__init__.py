@@ -214,6 +214,11 @@ def to_ref_layers(layers: Sequence) -> tuple:
         elif name == "ChannelAffine":
             c.kind = 3
             s, t = np.ascontiguousarray(l.scale, np.float32), np.ascontiguousarray(l.shift, np.float32)
+            # fold_batch_norm and the lone affine index shift[c] for every
+            # c < scale.len() (mod.rs:236-237, 246; npu.rs:254-268): a shorter
+            # shift is an index panic there, a longer one is read no further
+            if t.size < s.size:
+                raise ValueError("ChannelAffine: shift shorter than scale (the reference panics)")
             c.scale, c.shift, c.affine_len = _fp(s), _fp(t), s.size
             keep += [s, t]
         elif name == "MaxPool2d":

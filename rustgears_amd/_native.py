@@ -26,6 +26,7 @@ LAYER_LINEAR, LAYER_CONV2D, LAYER_CHANNEL_AFFINE = 1, 2, 3
 LAYER_MAXPOOL2D, LAYER_FLATTEN, LAYER_ACTIVATION, LAYER_SOFTMAX = 4, 5, 6, 7
 PRECISION_INT8, PRECISION_FP16, PRECISION_FP32 = 0, 1, 2
 CAP_QACT, CAP_SCALE, CAP_ACC, CAP_OUT = 0, 1, 2, 3
+CAPTURE_OFF, CAPTURE_FULL, CAPTURE_PRODUCTION = 0, 1, 2
 
 f32p = ctypes.POINTER(ctypes.c_float)
 i64p = ctypes.POINTER(ctypes.c_int64)
@@ -37,14 +38,15 @@ class CLayer(ctypes.Structure):
 
     _fields_ = [
         ("kind", ctypes.c_int32),
-        ("in_features", ctypes.c_int32), ("out_features", ctypes.c_int32),
-        ("in_channels", ctypes.c_int32), ("out_channels", ctypes.c_int32),
-        ("kernel", ctypes.c_int32), ("stride", ctypes.c_int32), ("padding", ctypes.c_int32),
-        ("pool_kernel", ctypes.c_int32), ("pool_stride", ctypes.c_int32),
         ("act", ctypes.c_int32), ("act_param", ctypes.c_float),
+        ("in_features", ctypes.c_int64), ("out_features", ctypes.c_int64),
+        ("in_channels", ctypes.c_int64), ("out_channels", ctypes.c_int64),
+        ("kernel", ctypes.c_int64), ("stride", ctypes.c_int64), ("padding", ctypes.c_int64),
+        ("pool_kernel", ctypes.c_int64), ("pool_stride", ctypes.c_int64),
         ("weight", f32p), ("weight_len", ctypes.c_int64),
         ("bias", f32p), ("bias_len", ctypes.c_int64),
-        ("scale", f32p), ("shift", f32p), ("affine_len", ctypes.c_int64),
+        ("scale", f32p), ("scale_len", ctypes.c_int64),
+        ("shift", f32p), ("shift_len", ctypes.c_int64),
     ]
 
 

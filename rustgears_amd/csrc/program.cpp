@@ -187,6 +187,12 @@ struct Plan {
   std::vector<uint8_t> mask_host;
   std::vector<std::unique_ptr<DevBuf>> cap_q, cap_acc, cap_out;
   bool capture_ready = false;
+  // Production taps (test only): per op, a copy of its absmax slot words and
+  // whether its i8 operand (cap_q) and f32 output (cap_out) exist in memory
+  // on the production path.
+  std::vector<std::unique_ptr<DevBuf>> tap_slot;
+  std::vector<uint8_t> tap_q_ok, tap_out_ok;
+  bool taps_ready = false;
   // Per op, indices into the run's launch events (-1 = the run-start event):
   // [0] last launch before the op, [1] last launch before its main kernel,
   // [2] its main kernel (== [1] when the op launches none).
@@ -210,6 +216,11 @@ struct rgnpu_program {
   int profiling = 1;
   bool capture = false;
   bool capture_valid = false;
+  // Production taps: the production plan and kernels run unchanged, and the
+  // operands, absmax slots and outputs that exist in memory are copied after
+  // each op (rgnpu_program_set_capture(prog, RGNPU_CAPTURE_PRODUCTION)).
+  bool taps = false;
+  bool taps_valid = false;
   std::vector<hipEvent_t> ev;  // run start/end + launch events
   bool profile_pending = false;
   bool have_profile = false;
@@ -240,25 +251,39 @@ namespace rgnpu {
 
 static void check_layer(const rgnpu_layer& l, int64_t idx) {
   auto bad = [&](const std::string& m) { throw Error(RGNPU_ERR_INVALID, "layer " + std::to_string(idx) + ": " + m); };
+  // Every size the kernels index with fits 31 bits; the ABI fields are 64-bit
+  // only so that any u32 of an .rtim file reads back unchanged.
+  constexpr int64_t kMaxField = INT32_MAX;
+  auto too_big = [&](std::initializer_list<int64_t> v) {
+    for (int64_t x : v)
+      if (x > kMaxField) bad("size field above 2^31 - 1 is not supported");
+  };
   switch (l.kind) {
     case RGNPU_LAYER_LINEAR:
+      too_big({l.in_features, l.out_features});
       if (l.in_features <= 0 || l.out_features <= 0) bad("Linear needs positive in/out features");
       // the GEMM epilogue addresses 16 output rows with 32-bit byte offsets
       if (l.out_features > (1 << 26)) bad("Linear out_features above 2^26 are not supported");
-      if (l.weight_len != (int64_t)l.in_features * l.out_features || !l.weight) bad("Linear weight must be [in, out]");
+      if (l.weight_len != l.in_features * l.out_features || !l.weight) bad("Linear weight must be [in, out]");
       if (l.bias_len != l.out_features || !l.bias) bad("Linear bias must have out_features elements");
       break;
     case RGNPU_LAYER_CONV2D:
+      too_big({l.in_channels, l.out_channels, l.kernel, l.stride, l.padding});
       if (l.in_channels <= 0 || l.out_channels <= 0 || l.kernel <= 0 || l.stride <= 0 || l.padding < 0)
         bad("Conv2d needs positive channels/kernel/stride and padding >= 0");
-      if (l.weight_len != (int64_t)l.out_channels * l.in_channels * l.kernel * l.kernel || !l.weight)
+      if ((__int128)l.weight_len != (__int128)l.out_channels * l.in_channels * l.kernel * l.kernel || !l.weight)
         bad("Conv2d weight must be [out, in, k, k]");
       if (l.bias_len != l.out_channels || !l.bias) bad("Conv2d bias must have out_channels elements");
       break;
     case RGNPU_LAYER_CHANNEL_AFFINE:
-      if (l.affine_len <= 0 || !l.scale || !l.shift) bad("ChannelAffine needs scale and shift");
+      too_big({l.scale_len});
+      if (l.scale_len <= 0 || !l.scale || !l.shift) bad("ChannelAffine needs scale and shift");
+      // fold_batch_norm and the lone affine read shift[c] for c < scale.len()
+      // (mod.rs:236-237, 246, 302; npu.rs:254-268): a shorter shift panics there
+      if (l.shift_len < l.scale_len) bad("ChannelAffine shift is shorter than its scale");
       break;
     case RGNPU_LAYER_MAXPOOL2D:
+      too_big({l.pool_kernel, l.pool_stride});
       if (l.pool_kernel <= 0 || l.pool_stride <= 0) bad("MaxPool2d needs positive kernel and stride");
       break;
     case RGNPU_LAYER_FLATTEN:
@@ -285,7 +310,7 @@ static std::vector<FLayer> fold_batch_norm(const rgnpu_layer* L, int64_t n) {
     const rgnpu_layer& l = L[i];
     if (l.kind == RGNPU_LAYER_CHANNEL_AFFINE && !out.empty()) {
       FLayer& last = out.back();
-      if (last.spec.kind == RGNPU_LAYER_LINEAR && last.spec.out_features == l.affine_len) {
+      if (last.spec.kind == RGNPU_LAYER_LINEAR && last.spec.out_features == l.scale_len) {
         const int64_t in = last.spec.in_features, of = last.spec.out_features;
         for (int64_t r = 0; r < in; r++)
           for (int64_t c = 0; c < of; c++) last.w[r * of + c] = last.w[r * of + c] * l.scale[c];
@@ -295,7 +320,7 @@ static std::vector<FLayer> fold_batch_norm(const rgnpu_layer* L, int64_t n) {
         }
         continue;
       }
-      if (last.spec.kind == RGNPU_LAYER_CONV2D && last.spec.out_channels == l.affine_len) {
+      if (last.spec.kind == RGNPU_LAYER_CONV2D && last.spec.out_channels == l.scale_len) {
         const int64_t plane = (int64_t)last.spec.in_channels * last.spec.kernel * last.spec.kernel;
         for (int64_t o = 0; o < last.spec.out_channels; o++) {
           for (int64_t j = 0; j < plane; j++) last.w[o * plane + j] = last.w[o * plane + j] * l.scale[o];
@@ -311,8 +336,9 @@ static std::vector<FLayer> fold_batch_norm(const rgnpu_layer* L, int64_t n) {
       f.w.assign(l.weight, l.weight + l.weight_len);
       f.b.assign(l.bias, l.bias + l.bias_len);
     } else if (l.kind == RGNPU_LAYER_CHANNEL_AFFINE) {
-      f.scale.assign(l.scale, l.scale + l.affine_len);
-      f.shift.assign(l.shift, l.shift + l.affine_len);
+      // entries of a longer shift past scale.len() are never read
+      f.scale.assign(l.scale, l.scale + l.scale_len);
+      f.shift.assign(l.shift, l.shift + l.scale_len);
     }
     out.push_back(std::move(f));
   }
@@ -498,8 +524,7 @@ static void compile_standard(rgnpu_program* P, const std::vector<FLayer>& F) {
 // npu::compile (npu.rs:188-276).
 static void compile(rgnpu_program* P, const rgnpu_layer* layers, int64_t n) {
   const bool f16 = P->precision == RGNPU_PRECISION_FP16;
-  for (int64_t i = 0; i < n; i++) check_layer(layers[i], i);
-  P->original_layers = n;
+  P->original_layers = n;  // every layer passed check_layer in rgnpu_program_create
   std::vector<FLayer> F = fold_batch_norm(layers, n);
   if (P->precision == RGNPU_PRECISION_FP32) {
     compile_standard(P, F);
@@ -974,6 +999,32 @@ static void ensure_capture_buffers(rgnpu_program* P, Plan& plan) {
   plan.capture_ready = true;
 }
 
+// Buffers of the production taps: the INT8 Linear operands, the absmax slot
+// words of every quantizing op, and every f32 output.
+static void ensure_tap_buffers(rgnpu_program* P, Plan& plan) {
+  if (plan.taps_ready) return;
+  const size_t n = P->ops.size();
+  plan.cap_q.resize(n);
+  plan.cap_out.resize(n);
+  plan.tap_slot.resize(n);
+  plan.tap_q_ok.assign(n, 0);
+  plan.tap_out_ok.assign(n, 0);
+  for (size_t i = 0; i < n; i++) {
+    const Op& op = *P->ops[i];
+    const OpPlan& pl = plan.ops[i];
+    plan.cap_out[i] = std::make_unique<DevBuf>();
+    plan.cap_out[i]->ensure((size_t)pl.out_len * sizeof(float));
+    if (pl.slot_base < 0) continue;
+    plan.tap_slot[i] = std::make_unique<DevBuf>();
+    plan.tap_slot[i]->ensure((size_t)(op.kind == OP_LINEAR ? kTensorSlotWords : pl.slot_count) * sizeof(uint32_t));
+    if (op.kind == OP_LINEAR) {
+      plan.cap_q[i] = std::make_unique<DevBuf>();
+      plan.cap_q[i]->ensure((size_t)(pl.Mpad * op.Kpad));
+    }
+  }
+  plan.taps_ready = true;
+}
+
 static void finalize_profile(rgnpu_program* P);
 
 static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
@@ -1037,12 +1088,16 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
   const bool f16 = P->precision == RGNPU_PRECISION_FP16;
   const bool f32 = P->precision == RGNPU_PRECISION_FP32;
   const bool cap = P->capture;
+  // production taps: copies between the unchanged launches (not in the
+  // allocation-free plan, whose buffers other calls share)
+  const bool tap = P->taps && !cap && !plan.in_scratch;
   struct SinkOff {
     ~SinkOff() { set_launch_events(nullptr, 0); }
   } sink_off;
   timed = timed && ev;
   set_launch_events(timed ? ev + 2 : nullptr, timed ? (int)launch_event_cap(P) : 0);
   if (cap) ensure_capture_buffers(P, plan);
+  if (tap) ensure_tap_buffers(P, plan);
   plan.roles.assign(P->ops.size(), std::array<int, 3>{-1, -1, -1});
   if (ev) RG_HIP(hipEventRecord(ev[0], s));
   if (plan.in_scratch && !plan.mask_host.empty())
@@ -1205,6 +1260,12 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           }
         }
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, qa, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
+        // the one-row GEMV and the narrow GEMM that quantize as they read
+        // leave no i8 operand in memory
+        if (tap && pl.rows > 0 && !narrow_xq && !gemv_xq) {
+          RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, qa, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
+          plan.tap_q_ok[i] = 1;
+        }
         break;
       }
       case OP_CONV: {
@@ -1341,6 +1402,23 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     if (cap)
       RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),
                             hipMemcpyDeviceToDevice, s));
+    if (tap) {
+      if (pl.slot_base >= 0) {
+        const int64_t words = op.kind == OP_LINEAR ? kTensorSlotWords : pl.slot_count;
+        RG_HIP(hipMemcpyAsync(plan.tap_slot[i]->p, slots + pl.slot_base, (size_t)words * sizeof(uint32_t),
+                              hipMemcpyDeviceToDevice, s));
+      }
+      // The op's own f32 output exists unless its GEMM hands the next op its
+      // operand instead (INT8 requantization, FP16 hand-off), or the conv
+      // pools in its epilogue (its buffer then holds the pool's output, which
+      // is the output of the MaxPool2d op; an FP32 conv's absorbed Act op
+      // likewise has none of its own).
+      const bool has_out = !pl.requant && !pl.handoff && !pl.pool_r16 && !(pl.pool_fused && op.kind != OP_POOL);
+      plan.tap_out_ok[i] = has_out;
+      if (has_out && pl.out_len > 0)
+        RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),
+                              hipMemcpyDeviceToDevice, s));
+    }
     const int end = launch_events_used();
     plan.roles[i] = {first - 1, pre - 1, end > pre ? end - 1 : pre - 1};
   }
@@ -1352,7 +1430,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
   if (!any && plan.out_len > 0)
     RG_HIP(hipMemcpyAsync(y, x, (size_t)plan.out_len * sizeof(float), hipMemcpyDeviceToDevice, s));
   if (ev) RG_HIP(hipEventRecord(ev[1], s));
-  P->capture_valid = cap;
+  P->capture_valid = cap || tap;
+  P->taps_valid = tap;
 }
 
 static void enqueue_profiled(rgnpu_program* P, Plan& plan, const float* x, float* y) {
@@ -1433,6 +1512,9 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
   if (n_layers < 0 || (n_layers > 0 && !layers)) throw Error(RGNPU_ERR_INVALID, "invalid layer list");
   if (precision != RGNPU_PRECISION_INT8 && precision != RGNPU_PRECISION_FP16 && precision != RGNPU_PRECISION_FP32)
     throw Error(RGNPU_ERR_INVALID, "unknown precision");
+  // the layer list is checked before any device work, so a bad spec gives
+  // RGNPU_ERR_INVALID on any machine
+  for (int64_t i = 0; i < n_layers; i++) check_layer(layers[i], i);
   int count = 0;
   RG_HIP(hipGetDeviceCount(&count));
   if (device < 0 || device >= count) throw Error(RGNPU_ERR_DEVICE, "device index out of range");
@@ -1551,11 +1633,11 @@ int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, in
   int profiling;
   {
     std::lock_guard<std::mutex> lk(P->mu);
-    capture = P->capture;
+    capture = P->capture || P->taps;
     profiling = P->profiling;
   }
   if (capture) {
-    // capture taps live on the handle's own plan
+    // capture and production taps live on the handle's own plan
     run_host(P, x, shape, ndim, y, y_cap, y_shape, y_ndim);
     return RGNPU_OK;
   }
@@ -1600,7 +1682,7 @@ int rgnpu_program_run_device_noalloc(rgnpu_program* P, const float* d_x, const i
   RG_API_BEGIN
   if (!P || !shape) throw Error(RGNPU_ERR_INVALID, "NULL argument");
   std::lock_guard<std::mutex> lk(P->mu);
-  if (P->capture)
+  if (P->capture || P->taps)
     throw Error(RGNPU_ERR_INVALID, "capture mode allocates its tap buffers: use rgnpu_program_run_device");
   if (!P->scratch) throw Error(RGNPU_ERR_DEVICE, "no device scratch for this program");
   RG_HIP(hipSetDevice(P->device));
@@ -1627,6 +1709,7 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
   if (!P || !shape || !d_y || iters <= 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
   const bool per_kernel_events = (flags & RGNPU_BENCH_KERNEL_EVENTS) != 0;
   std::lock_guard<std::mutex> lk(P->mu);
+  if (P->capture || P->taps) throw Error(RGNPU_ERR_INVALID, "capture mode is on: benchmark times the production path only");
   RG_HIP(hipSetDevice(P->device));
   Plan& plan = get_plan(P, shape, ndim);
   if (y_cap < plan.out_len) throw Error(RGNPU_ERR_CAPACITY, "output buffer too small");
@@ -1767,9 +1850,12 @@ int64_t rgnpu_program_summary(const rgnpu_program* P, char* buf, int64_t cap) {
 int rgnpu_program_set_capture(rgnpu_program* P, int32_t on) {
   RG_API_BEGIN
   if (!P) throw Error(RGNPU_ERR_INVALID, "NULL program");
+  if (on < RGNPU_CAPTURE_OFF || on > RGNPU_CAPTURE_PRODUCTION) throw Error(RGNPU_ERR_INVALID, "unknown capture mode");
   std::lock_guard<std::mutex> lk(P->mu);
-  P->capture = on != 0;
-  if (!P->capture) P->capture_valid = false;
+  P->capture = on == RGNPU_CAPTURE_FULL;
+  P->taps = on == RGNPU_CAPTURE_PRODUCTION;
+  P->capture_valid = false;
+  P->taps_valid = false;
   RG_API_END
 }
 
@@ -1798,6 +1884,39 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
       }
       return count;
     };
+    if (P->taps_valid) {
+      switch (what) {
+        case RGNPU_CAP_OUT:
+          if (!plan.tap_out_ok[(size_t)i]) return 0;
+          return copy_out(plan.cap_out[(size_t)i]->p, pl.out_len, sizeof(float));
+        case RGNPU_CAP_ACC:
+          return 0;  // the i32 sums never leave the GEMM's registers
+        case RGNPU_CAP_SCALE: {
+          if (!gemm) return 0;
+          // the scale each consumer derives from the absmax slot that its
+          // producer (or its own absmax pass) filled
+          const bool lin = op.kind == OP_LINEAR;
+          std::vector<uint32_t> w((size_t)(lin ? kTensorSlotWords : pl.slot_count));
+          RG_HIP(hipMemcpy(w.data(), plan.tap_slot[(size_t)i]->p, w.size() * sizeof(uint32_t), hipMemcpyDeviceToHost));
+          std::vector<float> sc;
+          if (lin) {
+            uint32_t m = 0;
+            for (int k = 0; k < kSpread; k++) m = std::max(m, w[(size_t)k * kSpreadStride]);
+            sc.push_back(rgmath::scale_from_absmax(rgmath::bitsf(m)));
+          } else {
+            for (uint32_t m : w) sc.push_back(rgmath::scale_from_absmax(rgmath::bitsf(m)));
+          }
+          const int64_t b = std::min<int64_t>(cap_bytes, (int64_t)(sc.size() * sizeof(float)));
+          if (dst && b > 0) std::memcpy(dst, sc.data(), (size_t)b);
+          return (int64_t)sc.size();
+        }
+        case RGNPU_CAP_QACT:
+          if (!gemm || op.kind != OP_LINEAR || !plan.tap_q_ok[(size_t)i]) return 0;
+          break;  // the Linear operand, read back as in capture mode
+        default:
+          return -1;
+      }
+    }
     switch (what) {
       case RGNPU_CAP_OUT:
         return copy_out(plan.cap_out[(size_t)i]->p, pl.out_len, sizeof(float));

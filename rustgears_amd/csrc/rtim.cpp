@@ -107,10 +107,10 @@ int rgnpu_rtim_load(const char* path, rgnpu_rtim** out_handle, const rgnpu_layer
       const uint32_t tag = r.u32();
       if (!r.ok) break;
       switch (tag) {
-        case 1:
+        case 1:  // u32 fields read as the reference's usize: every value fits the int64 fields
           L.kind = RGNPU_LAYER_LINEAR;
-          L.in_features = (int32_t)r.u32();
-          L.out_features = (int32_t)r.u32();
+          L.in_features = r.u32();
+          L.out_features = r.u32();
           L.weight = vec();
           L.weight_len = (int64_t)h->arrays.back()->size();
           L.bias = vec();
@@ -118,30 +118,27 @@ int rgnpu_rtim_load(const char* path, rgnpu_rtim** out_handle, const rgnpu_layer
           break;
         case 2:
           L.kind = RGNPU_LAYER_CONV2D;
-          L.in_channels = (int32_t)r.u32();
-          L.out_channels = (int32_t)r.u32();
-          L.kernel = (int32_t)r.u32();
-          L.stride = (int32_t)r.u32();
-          L.padding = (int32_t)r.u32();
+          L.in_channels = r.u32();
+          L.out_channels = r.u32();
+          L.kernel = r.u32();
+          L.stride = r.u32();
+          L.padding = r.u32();
           L.weight = vec();
           L.weight_len = (int64_t)h->arrays.back()->size();
           L.bias = vec();
           L.bias_len = (int64_t)h->arrays.back()->size();
           break;
-        case 3:
+        case 3:  // two independent vectors, lengths not compared (save.rs:254)
           L.kind = RGNPU_LAYER_CHANNEL_AFFINE;
           L.scale = vec();
-          L.affine_len = (int64_t)h->arrays.back()->size();
+          L.scale_len = (int64_t)h->arrays.back()->size();
           L.shift = vec();
-          if ((int64_t)h->arrays.back()->size() != L.affine_len && r.ok) {
-            status = RGNPU_ERR_FORMAT;
-            err = "ChannelAffine scale/shift length mismatch";
-          }
+          L.shift_len = (int64_t)h->arrays.back()->size();
           break;
         case 4:
           L.kind = RGNPU_LAYER_MAXPOOL2D;
-          L.pool_kernel = (int32_t)r.u32();
-          L.pool_stride = (int32_t)r.u32();
+          L.pool_kernel = r.u32();
+          L.pool_stride = r.u32();
           break;
         case 5:
           L.kind = RGNPU_LAYER_FLATTEN;
@@ -228,7 +225,7 @@ int rgnpu_rtim_save(const char* path, const rgnpu_layer* layers, int64_t n_layer
         w.vec(L.weight, L.weight_len); w.vec(L.bias, L.bias_len);
         break;
       case RGNPU_LAYER_CHANNEL_AFFINE:
-        w.u32(3); w.vec(L.scale, L.affine_len); w.vec(L.shift, L.affine_len);
+        w.u32(3); w.vec(L.scale, L.scale_len); w.vec(L.shift, L.shift_len);
         break;
       case RGNPU_LAYER_MAXPOOL2D:
         w.u32(4); w.u32((uint32_t)L.pool_kernel); w.u32((uint32_t)L.pool_stride);

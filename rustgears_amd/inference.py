@@ -158,7 +158,8 @@ def to_c_layers(layers: Sequence[AnyLayer]):
             keep += [l.weight, l.bias]
         elif isinstance(l, LayerSpec.ChannelAffine):
             c.kind = N.LAYER_CHANNEL_AFFINE
-            c.scale, c.shift, c.affine_len = _ptr(l.scale), _ptr(l.shift), l.scale.size
+            c.scale, c.scale_len = _ptr(l.scale), l.scale.size
+            c.shift, c.shift_len = _ptr(l.shift), l.shift.size
             keep += [l.scale, l.shift]
         elif isinstance(l, LayerSpec.MaxPool2d):
             c.kind = N.LAYER_MAXPOOL2D
@@ -190,7 +191,7 @@ def from_c_layers(ptr, n: int) -> List[AnyLayer]:
             out.append(LayerSpec.Conv2d(c.in_channels, c.out_channels, c.kernel, c.stride, c.padding,
                                         vec(c.weight, c.weight_len), vec(c.bias, c.bias_len)))
         elif c.kind == N.LAYER_CHANNEL_AFFINE:
-            out.append(LayerSpec.ChannelAffine(vec(c.scale, c.affine_len), vec(c.shift, c.affine_len)))
+            out.append(LayerSpec.ChannelAffine(vec(c.scale, c.scale_len), vec(c.shift, c.shift_len)))
         elif c.kind == N.LAYER_MAXPOOL2D:
             out.append(LayerSpec.MaxPool2d(c.pool_kernel, c.pool_stride))
         elif c.kind == N.LAYER_FLATTEN:
@@ -483,8 +484,13 @@ class InferenceSession:
                           int(hdr.npu_weight_bytes), int(hdr.total_macs), int(hdr.total_ns), records)
 
     # ---- capture taps ------------------------------------------------------
-    def set_capture(self, on: bool) -> None:
-        N.check(N.lib().rgnpu_program_set_capture(self._h, 1 if on else 0))
+    def set_capture(self, on) -> None:
+        """True: capture taps (capture kernels: every op's i8 activations,
+        scales, i32 sums and f32 output).  "production": production taps
+        (the production kernels unchanged; what exists in memory between
+        them is copied).  False: off."""
+        mode = N.CAPTURE_PRODUCTION if on == "production" else (N.CAPTURE_FULL if on else N.CAPTURE_OFF)
+        N.check(N.lib().rgnpu_program_set_capture(self._h, mode))
 
     def capture(self, op: int, what: int) -> np.ndarray:
         dtype = {N.CAP_QACT: np.int8, N.CAP_SCALE: np.float32, N.CAP_ACC: np.int32, N.CAP_OUT: np.float32}[what]

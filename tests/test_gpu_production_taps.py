@@ -1,0 +1,107 @@
+"""Production taps: the kernels the benchmark times, checked operand by operand.
+
+Capture mode switches kernels to their capture forms (exact GELU everywhere,
+no conv + pool fusion, every f32 output stored).  Production taps
+(set_capture("production"), RGNPU_CAPTURE_PRODUCTION) keep the production
+plan and kernels unchanged and copy, device to device between launches, what
+exists in memory after each op:
+
+* the i8 operand a Linear's GEMM read -- written by the one-pass input
+  quantization (npu.rs:312 -> quantize.rs:18-24 on the run's input) or by the
+  previous GEMM's fused requantization, with the certified GELU form for
+  GELU producers;
+* the scale every quantizing op derived from its absmax slot (per tensor for
+  a Linear, per image for a conv, npu.rs:346-351);
+* the f32 output of every op that stores one (the conv + pool kernel stores
+  only the pooled output: the MaxPool2d op's).
+
+Each is compared bit for bit with the oracle's capture of the same op, at
+the benchmark's full sizes: the 4 x 4096^2 GELU stack (8192 rows), the deep
+MLP (4096 rows) and the CNN (256 images).
+"""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_production(rg, ref, layers, x, what, want_q, want_out):
+    """Runs the production path with taps and the oracle with capture; checks
+    every available tap and that exactly the expected ones exist (want_q /
+    want_out: op indices with an i8 operand / an f32 output in memory)."""
+    print(f"[taps] {what} x{tuple(x.shape)}", flush=True)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y_plain = sess.run(x)
+    sess.set_capture("production")
+    y = sess.run(x)
+    prof = sess.last_npu_profile()
+    prog = ref.RefProgram(layers)
+    prog.set_capture(True)
+    yr = prog.run(x, parallel=True)
+    assert sess.op_labels() == prog.labels(), what
+    have_q, have_out, checked = [], [], 0
+    for i in range(prog.num_ops):
+        tag = f"{what} op{i} ({prog.labels()[i]})"
+        assert sess.capture(i, 2).size == 0, tag + ": no i32 sums on the production path"
+        q = sess.capture(i, 0)
+        if q.size:
+            have_q.append(i)
+            want = prog.capture(i, 0)
+            assert q.shape == want.shape and np.array_equal(q, want), \
+                f"{tag} qact: {np.count_nonzero(q != want)} of {want.size} differ"
+            checked += q.size
+        s = sess.capture(i, 1)
+        ws = prog.capture(i, 1)
+        if ws.size:
+            assert_bitexact_f32(s, ws, tag + " scale")
+        o = sess.capture(i, 3)
+        if o.size:
+            have_out.append(i)
+            assert_bitexact_f32(o, prog.capture(i, 3), tag + " out")
+    assert have_q == want_q, (what, have_q)
+    assert have_out == want_out, (what, have_out)
+    assert_bitexact_f32(y, yr, what + " output")
+    assert_bitexact_f32(y_plain, yr, what + " output without taps")
+    sess.close()
+    print(f"[taps] {what}: {checked} i8 operand bytes bit-exact", flush=True)
+    return prof
+
+
+def test_linear_stack_production_operands(rg, ref):
+    """S: layer 1's operand from the one-pass input quantization, layers 2-4's
+    from the fused requantization with the certified GELU; only the last
+    layer stores an f32 output."""
+    from rustgears_amd import configs
+    model, x = configs.linear_stack()
+    prof = _check_production(rg, ref, model.export(), x, "stack 4x4096 gelu", [0, 1, 2, 3], [3])
+    for r in prof.records[1:]:
+        assert r.duration_ns == r.kernel_ns, r  # fused: nothing launched before the GEMM
+
+
+def test_deep_mlp_production_operands(rg, ref):
+    """D: 784 -> 1024 quantizes its own input in one pass; the 1024 -> 1024
+    layer and the head read operands from their producers' requantization."""
+    from rustgears_amd import configs
+    model, x = configs.deep_mlp()
+    _check_production(rg, ref, model.export(), x, "deep mlp", [0, 1, 2], [2])
+
+
+def test_cnn_production_operands(rg, ref):
+    """C: both convs quantize their f32 input into LDS and pool in their
+    epilogue (no i8 image, no conv output in memory: the MaxPool2d ops hold
+    the pooled outputs); the per-image scales come from conv1's own absmax
+    and from pool 1's fused absmax; the fc layer's operand comes from
+    quant_rows with pool 2's absmax, the head quantizes as it reads."""
+    from rustgears_amd import configs
+    model, x = configs.cnn()
+    layers = model.export()
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    labels = sess.op_labels()
+    sess.close()
+    # conv, pool, conv, pool, flatten, fc, head
+    assert [l.split("(")[0] for l in labels] == ["NPU::FusedConv2dAct", "NPU::MaxPool2d", "NPU::FusedConv2dAct",
+                                                 "NPU::MaxPool2d", "NPU::Flatten", "NPU::FusedGemmAct",
+                                                 "NPU::Gemm"], labels
+    _check_production(rg, ref, layers, x, "cnn", [5], [1, 3, 4, 5, 6])
