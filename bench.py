@@ -364,7 +364,11 @@ def main():
         conc_s = time.perf_counter() - h0
     line["pcie_inclusive_concurrent"] = {
         "value": round(n_conc * batch / conc_s, 2), "unit": "samples/s", "threads": threads,
-        "runs": n_conc, "note": "host-pointer run() from several threads on one session, wall clock"}
+        "runs": n_conc, "note": "host-pointer run() from several threads on one session, wall clock",
+        # cumulative over the session (all runs above): workgroups of the
+        # persistent grids that gave up waiting at the barrier and deferred
+        # their quantization, and finished barrier launches
+        "barrier": sess.barrier_stats()}
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, args.precision)
         line["cpu_baseline"]["host"] = host_description()

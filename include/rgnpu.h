@@ -268,6 +268,26 @@ void rgnpu_fill_normal(float* out, int64_t n);                           /* Tens
  * ceiling that the GEMM kernels' MFMA utilization is compared against. */
 int rgnpu_probe_mfma_rate(int32_t device, int64_t iters, int32_t random_operands, double* ms, double* tops);
 
+/* Cost of one poll of the persistent grids' barrier (one s_sleep of 512
+ * clocks and one agent-scope atomic load of a 128-byte line): thread 0 of
+ * each of `blocks` workgroups polls a line of its own that is never set,
+ * `polls` times, in one launch timed with HIP events.  No counterpart in the
+ * reference: it states in microseconds the barrier's wait bound
+ * (RGNPU_REQUANT_SPIN_LIMIT polls, default 100000). */
+int rgnpu_probe_barrier_poll(int32_t device, int32_t blocks, int32_t polls, double* us_per_poll);
+
+/* Cumulative counters of the persistent grids' barriers (the fused
+ * requantization and the one-pass input quantization) over a program's
+ * handle and its idle workers since creation: workgroups that gave up
+ * waiting and deferred their quantization to the finisher (correct results,
+ * later), workgroups a finisher found unsettled (their outputs were not
+ * quantized; the synchronizing call of that run -- rgnpu_program_run,
+ * rgnpu_program_synchronize, rgnpu_program_benchmark -- returns
+ * RGNPU_ERR_DEVICE), and finished barrier launches.  Synchronizes the
+ * streams it reads.  No counterpart in the reference; a diagnostic for
+ * concurrent runs. */
+int rgnpu_program_barrier_stats(rgnpu_program* prog, uint64_t* deferred, uint64_t* unsettled, uint64_t* launches);
+
 int rgnpu_device_count(int32_t* count);
 int rgnpu_device_alloc(int32_t device, int64_t bytes, void** out);
 int rgnpu_device_free(void* p);

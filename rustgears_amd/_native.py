@@ -105,6 +105,10 @@ SIGNATURES = [
     ("rgnpu_fill_normal", None, [f32p, ctypes.c_int64]),
     ("rgnpu_probe_mfma_rate", ctypes.c_int, [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
                                              ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    ("rgnpu_probe_barrier_poll", ctypes.c_int, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                                ctypes.POINTER(ctypes.c_double)]),
+    ("rgnpu_program_barrier_stats", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64),
+                                                   ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
     ("rgnpu_device_count", ctypes.c_int, [i32p]),
     ("rgnpu_device_alloc", ctypes.c_int, [ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(ctypes.c_void_p)]),
     ("rgnpu_device_free", ctypes.c_int, [ctypes.c_void_p]),

@@ -239,6 +239,12 @@ struct rgnpu_program {
   std::vector<char> worker_busy;
   rgnpu::Staging staging;  // pinned ring for this stream's host copies
   DevBuf evict;            // zero buffer read between benchmark runs on request
+  // This context's cumulative barrier counters (kStat*, requant.hip), a
+  // pinned copy of them read after each synchronization, and the unsettled
+  // count already reported.
+  DevBuf stats;
+  uint32_t* stats_host = nullptr;
+  uint32_t unsettled_seen = 0;
 };
 
 // Bytes read between benchmark runs to displace the 256 MB memory-side cache.
@@ -909,7 +915,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     slots = pl.iq_sync_base + input_quant_sync_words(pl.Mpad, op.Kpad);
   }
   if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
-  else plan->spin_limit = 100000;  // ~20 ms
+  else plan->spin_limit = 100000;  // x kBarrierPollUs (0.32 us) = ~32 ms
   if (const char* e = getenv("RGNPU_GELU_CERT")) plan->gelu_cert = std::min(3, std::max(0, atoi(e)));
   plan->n_slots = slots;
   // The first computing op quantizes the input itself (its absmax is the
@@ -1026,6 +1032,33 @@ static void ensure_tap_buffers(rgnpu_program* P, Plan& plan) {
 }
 
 static void finalize_profile(rgnpu_program* P);
+
+// The barrier counters of a context: device words zeroed once, a pinned copy.
+static void init_stats(rgnpu_program* P) {
+  P->stats.ensure(kStatWords * sizeof(uint32_t));
+  launch_fill_u32(P->stats.as<uint32_t>(), kStatWords, 0u, P->stream);
+  RG_HIP(hipGetLastError());
+  RG_HIP(hipHostMalloc(reinterpret_cast<void**>(&P->stats_host), kStatWords * sizeof(uint32_t)));
+  for (int k = 0; k < kStatWords; k++) P->stats_host[k] = 0;
+}
+
+// After P's stream has drained past a copy of the counters into
+// stats_host: a finisher that met an unsettled workgroup left that
+// workgroup's share of the next operand unquantized, so the run is reported
+// as failed (once per occurrence).
+static void check_stats(rgnpu_program* P) {
+  const uint32_t u = P->stats_host[kStatUnsettled];
+  if (u != P->unsettled_seen) {
+    P->unsettled_seen = u;
+    throw Error(RGNPU_ERR_DEVICE, "a grid barrier workgroup never settled: the run's output is incomplete");
+  }
+}
+
+// Synchronous variant for the synchronizing entry points.
+static void read_stats(rgnpu_program* P) {
+  RG_HIP(hipMemcpyAsync(P->stats_host, P->stats.p, kStatWords * sizeof(uint32_t), hipMemcpyDeviceToHost, P->stream));
+  RG_HIP(hipStreamSynchronize(P->stream));
+}
 
 static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
   if (P->plan && (int)P->plan->in_shape.size() == ndim && P->plan->capture == P->capture &&
@@ -1209,7 +1242,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           // nothing before the GEMM
         } else if (pl.iq_sync_base >= 0) {
           launch_input_quant(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base,
-                             slots + pl.iq_sync_base, plan.spin_limit, clear, s);
+                             slots + pl.iq_sync_base, plan.spin_limit, P->stats.as<uint32_t>(), clear, s);
           first_launched();
         } else if (!pl.q_ready) {
           if (pl.explicit_absmax) {
@@ -1241,6 +1274,7 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             rq.keep_f32 = cap ? 1 : 0;
             rq.spin_limit = plan.spin_limit;
             rq.gelu_cert = plan.gelu_cert;
+            rq.stats = P->stats.as<uint32_t>();
             launch_gemm_requant(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, pl.Mpad, op.Npad, op.Kpad, ep, rq, s);
           } else if (gemv_xq) {
             launch_gemv_xq(in, op.d_w.as<int8_t>(), op.out_f, op.Npad, op.in_f, op.Kpad, ep, pl.explicit_absmax,
@@ -1529,6 +1563,7 @@ int rgnpu_program_create(const rgnpu_layer* layers, int64_t n_layers, int32_t pr
     RG_HIP(hipStreamSynchronize(P->stream));
     // this device's copy of the allocation-free entry point's scratch
     RG_HIP(scratch_address(device, &P->scratch));
+    init_stats(P.get());
     compile(P.get(), layers, n_layers);
   } catch (...) {
     (void)hipStreamDestroy(P->stream);
@@ -1551,6 +1586,7 @@ void rgnpu_program_destroy(rgnpu_program* P) {
   P->ops.clear();
   for (auto e : P->ev) (void)hipEventDestroy(e);
   if (P->stream) (void)hipStreamDestroy(P->stream);
+  if (P->stats_host) (void)hipHostFree(P->stats_host);
   delete P;
 }
 
@@ -1582,8 +1618,10 @@ static void run_host(rgnpu_program* P, const float* x, const int64_t* shape, int
   enqueue_profiled(P, plan, plan.host_in.as<float>(), plan.host_out.as<float>());
   if (plan.out_len > 0)
     RG_HIP(copy_to_host(P->staging, y, plan.host_out.p, (size_t)plan.out_len * sizeof(float), P->stream));
+  RG_HIP(hipMemcpyAsync(P->stats_host, P->stats.p, kStatWords * sizeof(uint32_t), hipMemcpyDeviceToHost, P->stream));
   RG_HIP(hipStreamSynchronize(P->stream));
   finalize_profile(P);
+  check_stats(P);
 }
 
 static rgnpu_program* acquire_worker(rgnpu_program* P) {
@@ -1604,6 +1642,7 @@ static rgnpu_program* acquire_worker(rgnpu_program* P) {
       W->ops = P->ops;
       RG_HIP(hipSetDevice(P->device));
       RG_HIP(hipStreamCreateWithFlags(&W->stream, hipStreamNonBlocking));
+      init_stats(W.get());
       P->workers.push_back(std::move(W));
       P->worker_busy.push_back(1);
       return P->workers.back().get();
@@ -1750,6 +1789,8 @@ int rgnpu_program_benchmark(rgnpu_program* P, const float* d_x, const int64_t* s
   float ms = 0.0f;
   RG_HIP(hipEventElapsedTime(&ms, t0, t1));
   if (total_ms) *total_ms = ms;
+  read_stats(P);
+  check_stats(P);
   if (avg) {
     for (size_t i = 0; i < P->ops.size() && (int32_t)i < cap; i++) {
       rgnpu_op_record r{};
@@ -1779,6 +1820,8 @@ int rgnpu_program_synchronize(rgnpu_program* P) {
   RG_HIP(hipSetDevice(P->device));
   RG_HIP(hipStreamSynchronize(P->stream));
   if (P->plan) finalize_profile(P);
+  read_stats(P);
+  check_stats(P);
   RG_API_END
 }
 
@@ -1972,6 +2015,59 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
     rgnpu::g_last_error = e.what();
     return -1;
   }
+}
+
+int rgnpu_program_barrier_stats(rgnpu_program* P, uint64_t* deferred, uint64_t* unsettled, uint64_t* launches) {
+  RG_API_BEGIN
+  if (!P) throw Error(RGNPU_ERR_INVALID, "NULL program");
+  uint64_t d = 0, u = 0, l = 0;
+  auto add = [&](rgnpu_program* C) {
+    RG_HIP(hipSetDevice(C->device));
+    RG_HIP(hipStreamSynchronize(C->stream));
+    uint32_t w[kStatWords];
+    RG_HIP(hipMemcpy(w, C->stats.p, sizeof w, hipMemcpyDeviceToHost));
+    d += w[kStatDeferred];
+    u += w[kStatUnsettled];
+    l += w[kStatLaunches];
+  };
+  {
+    std::lock_guard<std::mutex> lk(P->mu);
+    add(P);
+  }
+  {
+    // idle workers only: a busy one is mid-run on another thread
+    std::lock_guard<std::mutex> lk(P->pool_mu);
+    for (size_t i = 0; i < P->workers.size(); i++)
+      if (!P->worker_busy[i]) add(P->workers[i].get());
+  }
+  if (deferred) *deferred = d;
+  if (unsettled) *unsettled = u;
+  if (launches) *launches = l;
+  RG_API_END
+}
+
+int rgnpu_probe_barrier_poll(int32_t device, int32_t blocks, int32_t polls, double* us_per_poll) {
+  RG_API_BEGIN
+  if (!us_per_poll || blocks <= 0 || blocks > 4096 || polls <= 0) throw Error(RGNPU_ERR_INVALID, "invalid arguments");
+  RG_HIP(hipSetDevice(device));
+  DevBuf lines;
+  const int64_t words = (int64_t)blocks * 32;  // one 128-byte line per workgroup
+  lines.ensure((size_t)words * sizeof(uint32_t));
+  hipStream_t s = nullptr;
+  RG_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  struct Destroy {
+    hipStream_t s;
+    ~Destroy() { (void)hipStreamDestroy(s); }
+  } destroy{s};
+  load_code_object(s);
+  launch_fill_u32(lines.as<uint32_t>(), words, 0u, s);
+  RG_HIP(hipGetLastError());
+  RG_HIP(hipStreamSynchronize(s));
+  const double ms = probe_barrier_poll(lines.as<uint32_t>(), blocks, polls, s);
+  RG_HIP(hipStreamSynchronize(s));
+  if (ms <= 0) throw Error(RGNPU_ERR_DEVICE, "barrier poll probe failed");
+  *us_per_poll = ms * 1000.0 / polls;
+  RG_API_END
 }
 
 int rgnpu_probe_mfma_rate(int32_t device, int64_t iters, int32_t random_operands, double* ms, double* tops) {

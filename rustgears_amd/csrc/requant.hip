@@ -17,12 +17,34 @@
 //
 // The barrier wait is bounded.  On an otherwise idle device the G <= occupancy
 // workgroups are resident together, but a kernel on another stream may hold
-// CUs.  A workgroup that has polled spin_limit times (about 1 us each)
+// CUs.  A workgroup that has polled spin_limit times (kBarrierPollUs each)
 // stores its last tile's f32 outputs, marks itself deferred and exits; the
 // workgroup whose arrival completed the barrier (the finisher) waits for
-// every workgroup to settle (they are all running, so this is short) and
-// quantizes the deferred workgroups' tiles from memory.  No wait is
-// unbounded, so two such kernels can never deadlock each other.
+// every workgroup to settle (they have all arrived, so they are running and
+// each stores its state within spin_limit polls) and quantizes the deferred
+// workgroups' tiles from memory.  No wait is unbounded, so two such kernels
+// can never deadlock each other.  The context's counters (Requant::stats)
+// count deferrals, launches, and workgroups a finisher found unsettled after
+// its own, larger bound: the host turns the last into RGNPU_ERR_DEVICE.
+//
+// Memory ordering.  Everything that crosses workgroups on the common path is
+// an agent-scope atomic read-modify-write or atomic load: the absmax
+// partials, the arrival counters, the go lines and the state words.  On
+// gfx942/gfx950 these are performed with sc1 set, at the memory side where
+// every XCD sees them (LLVM AMDGPU memory model, GFX942 table: "atomicrmw /
+// load atomic, agent scope: sc1=1"), and a wave's earlier atomic has
+// completed before its next is issued once s_waitcnt vmcnt(0) has returned
+// (atomics without return are counted by vmcnt).  The partial's atomicMax is
+// waited for before the arrival, the finisher has observed every arrival
+// before it stores a go line, and a released workgroup loads the partials
+// only after it has observed its go line: each cross-workgroup value is read
+// by an atomic load after the atomic that wrote it has completed at the
+// memory side.  No plain (cached) load reads another workgroup's data except
+// on the deferral path, which fences (release before the deferred state,
+// acquire in the finisher).  Release/acquire orderings on the go lines
+// would make the compiler write back (buffer_wbl2) or invalidate
+// (buffer_inv) the XCD's L2 around every poll; the tests that force every
+// workgroup through the deferral path (spin limit 0) check the fenced path.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -60,6 +82,15 @@ static_assert(kError < kRequantStateBase, "state words follow the counters");
 // workgroup through its go line.  Returns 2 for the finisher, 1 for a
 // released workgroup, 0 for one that gave up after spin_limit polls.
 // blk_flag is a word of the workgroup's LDS.
+// One barrier poll loop: up to `limit` polls of a go line; true once set.
+__device__ __forceinline__ bool poll_go(const uint32_t* go, int limit) {
+  for (int k = 0; k < limit; k++) {
+    __builtin_amdgcn_s_sleep(rqk::kPollSleep);
+    if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return true;
+  }
+  return false;
+}
+
 __device__ __forceinline__ uint32_t grid_arrive(uint32_t* sync, int b, int G, int spin_limit, uint32_t* blk_flag) {
   if (threadIdx.x == 0) {
     const int g = b % rqk::kGroups;
@@ -70,11 +101,7 @@ __device__ __forceinline__ uint32_t grid_arrive(uint32_t* sync, int b, int G, in
             in_group &&
         __hip_atomic_fetch_add(sync + rqk::kGroupDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups)
       flag = 2;
-    uint32_t* const go = sync + rqk::kGoBase + (int64_t)b * rqk::kLine;
-    for (int k = 0; flag == 0 && k < spin_limit; k++) {
-      __builtin_amdgcn_s_sleep(rqk::kPollSleep);
-      if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) flag = 1;
-    }
+    if (flag == 0 && poll_go(sync + rqk::kGoBase + (int64_t)b * rqk::kLine, spin_limit)) flag = 1;
     *blk_flag = flag;
   }
   __syncthreads();
@@ -89,13 +116,17 @@ __device__ __forceinline__ uint32_t grid_arrive(uint32_t* sync, int b, int G, in
   return flag;
 }
 
-// The finisher's wait for every workgroup's state word (each is running, so
-// this is short; one that never settles raises the error flag): the indices
-// of the deferred ones go to list[0 .. *count).  Every thread calls it;
-// count is a word of LDS.
+// The finisher's wait for every workgroup's state word (each has arrived and
+// stores its state within spin_limit polls, so this is short; one that never
+// settles raises the error flag and the context's unsettled counter): the
+// indices of the deferred ones go to list[0 .. *count).  Every thread calls
+// it; count is a word of LDS.  Also counts the finished launch.
 __device__ __forceinline__ int collect_deferred(uint32_t* sync, int G, int spin_limit, uint32_t* list,
-                                                uint32_t* count) {
-  if (threadIdx.x == 0) *count = 0;
+                                                uint32_t* count, uint32_t* stats) {
+  if (threadIdx.x == 0) {
+    *count = 0;
+    if (stats) atomicAdd(stats + kStatLaunches, 1u);
+  }
   __syncthreads();
   for (int w = threadIdx.x; w < G; w += blockDim.x) {
     uint32_t st = 0;
@@ -104,7 +135,10 @@ __device__ __forceinline__ int collect_deferred(uint32_t* sync, int G, int spin_
       if (st != 0) break;
       __builtin_amdgcn_s_sleep(rqk::kPollSleep);
     }
-    if (st == 0) __hip_atomic_store(sync + rqk::kError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (st == 0) {
+      __hip_atomic_store(sync + rqk::kError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (stats) atomicAdd(stats + kStatUnsettled, 1u);
+    }
     if (st == rqk::kDeferred) list[atomicAdd(count, 1u)] = (uint32_t)w;
   }
   __syncthreads();
@@ -687,8 +721,10 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
     if (!rq.keep_f32 && !CAP) store_kept_f32<FM>(acc, ep.y, m0 + wrow, n0 + wcolw, N, sp_last, lane);
     __threadfence();
     __syncthreads();
-    if (tid == 0)
+    if (tid == 0) {
       __hip_atomic_store(rq.sync + kRequantStateBase + b, rqk::kDeferred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (rq.stats) atomicAdd(rq.stats + kStatDeferred, 1u);
+    }
     return;
   }
   if (tid == 0)
@@ -719,7 +755,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64, OCC) void gemm_requant_kern
   // Finisher: the scale tap, then the tiles of every deferred workgroup.
   if (tid == 0 && rq.scale_out) *rq.scale_out = scale;
   uint32_t* list = reinterpret_cast<uint32_t*>(smem);  // the ring is free: no K loop follows
-  const int ndef = collect_deferred(rq.sync, G, rq.spin_limit, list, &blk[1]);
+  const int ndef = collect_deferred(rq.sync, G, rq.spin_limit, list, &blk[1], rq.stats);
   if (ndef > 0) __threadfence();  // acquire: the deferred workgroups' stored outputs
   for (int d = 0; d < ndef; d++) {
     const int w = (int)list[d];
@@ -887,7 +923,7 @@ template <bool VEC, int U>
 __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* __restrict__ x, InputQuantShape sh,
                                                                    uint32_t* __restrict__ slot, int8_t* q,
                                                                    float* scale_out, uint32_t* sync, int spin_limit,
-                                                                   SlotClear clear) {
+                                                                   uint32_t* stats, SlotClear clear) {
   using namespace iq;
   constexpr int KL = lds_units(U), KR = U - KL;
   static_assert(KR <= kMaxRegUnits && (KL == 0 || KR >= kFirst) && (KL == 0 || KL % 2 == 1), "unit split");
@@ -969,8 +1005,10 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
     flag = grid_arrive(sync, b, G, spin_limit, &blk[0]);
     if (flag == 0) {
       // waited too long: the finisher quantizes this workgroup's units
-      if (tid == 0)
+      if (tid == 0) {
         __hip_atomic_store(sync + kRequantStateBase + b, rqk::kDeferred, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (stats) atomicAdd(stats + kStatDeferred, 1u);
+      }
       return;
     }
     if (tid == 0)
@@ -991,7 +1029,7 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   if (tid == 0 && scale_out) *scale_out = scale;
   if (G == 1) return;
   uint32_t* const list = blk + 16;  // kListWords words after the block state
-  const int ndef = collect_deferred(sync, G, spin_limit, list, &blk[1]);
+  const int ndef = collect_deferred(sync, G, spin_limit, list, &blk[1], stats);
   // the thread index again, from the wave index (scalar) and the lane count,
   // rather than a register held across the whole kernel
   const uint32_t tid2 = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 64u +
@@ -1044,25 +1082,28 @@ int64_t input_quant_sync_words(int64_t Mpad, int64_t Kpad) {
 
 template <bool VEC, int U>
 static void launch_iq(const float* x, const InputQuantShape& sh, int64_t G, uint32_t* slot, int8_t* q,
-                      float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+                      float* scale_out, uint32_t* sync, int spin_limit, uint32_t* stats, SlotClear clear,
+                      hipStream_t s) {
   RG_LAUNCH((input_quant_kernel<VEC, U>), dim3((unsigned)G), dim3(iq::kThreads), 0, s, x, sh, slot, q, scale_out, sync,
-            spin_limit, clear);
+            spin_limit, stats, clear);
 }
 
 template <bool VEC>
 static void launch_iq_u(int U, const float* x, const InputQuantShape& sh, int64_t G, uint32_t* slot, int8_t* q,
-                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+                        float* scale_out, uint32_t* sync, int spin_limit, uint32_t* stats, SlotClear clear,
+                        hipStream_t s) {
   switch (U) {
-    case 4: launch_iq<VEC, 4>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
-    case 8: launch_iq<VEC, 8>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
-    case 16: launch_iq<VEC, 16>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
-    case 32: launch_iq<VEC, 32>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
-    default: launch_iq<VEC, 64>(x, sh, G, slot, q, scale_out, sync, spin_limit, clear, s); break;
+    case 4: launch_iq<VEC, 4>(x, sh, G, slot, q, scale_out, sync, spin_limit, stats, clear, s); break;
+    case 8: launch_iq<VEC, 8>(x, sh, G, slot, q, scale_out, sync, spin_limit, stats, clear, s); break;
+    case 16: launch_iq<VEC, 16>(x, sh, G, slot, q, scale_out, sync, spin_limit, stats, clear, s); break;
+    case 32: launch_iq<VEC, 32>(x, sh, G, slot, q, scale_out, sync, spin_limit, stats, clear, s); break;
+    default: launch_iq<VEC, 64>(x, sh, G, slot, q, scale_out, sync, spin_limit, stats, clear, s); break;
   }
 }
 
 void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad, uint32_t* slot, int8_t* q,
-                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s) {
+                        float* scale_out, uint32_t* sync, int spin_limit, uint32_t* stats, SlotClear clear,
+                        hipStream_t s) {
   if (!input_quant_supported(M, K, Mpad, Kpad) || !slot || !q || !sync || (reinterpret_cast<uintptr_t>(q) & 15))
     throw std::logic_error("input_quant: unsupported shape or missing buffers");
   const bool vec = K % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -1072,9 +1113,33 @@ void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int6
                            (uint32_t)(iq::kThreads / upr), (uint32_t)(iq::kThreads % upr),
                            (uint32_t)(NT / upr), (uint32_t)(NT % upr)};
   if (vec)
-    launch_iq_u<true>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, clear, s);
+    launch_iq_u<true>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, stats, clear, s);
   else
-    launch_iq_u<false>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, clear, s);
+    launch_iq_u<false>(lc.U, x, sh, lc.G, slot, q, scale_out, sync, spin_limit, stats, clear, s);
+}
+
+// The poll probe: thread 0 of each workgroup runs the barrier's poll loop
+// `polls` times on a line of its own that nothing sets (zeroed by the
+// caller), so every poll runs; the other threads wait at the end.
+__global__ __launch_bounds__(256) void barrier_poll_probe_kernel(uint32_t* lines, int polls) {
+  if (threadIdx.x == 0 && poll_go(lines + (int64_t)blockIdx.x * rqk::kLine, polls)) lines[0] = 2u;
+}
+
+double probe_barrier_poll(uint32_t* lines, int blocks, int polls, hipStream_t s) {
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return -1.0;
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return -1.0;
+  }
+  (void)hipEventRecord(e0, s);
+  hipLaunchKernelGGL(barrier_poll_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, s, lines, polls);
+  (void)hipEventRecord(e1, s);
+  float ms = -1.0f;
+  if (hipGetLastError() == hipSuccess && hipEventSynchronize(e1) == hipSuccess) (void)hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return ms;
 }
 
 // This translation unit is its own code object: loaded at program creation

@@ -70,10 +70,30 @@ struct Requant {
   uint32_t* sync = nullptr;
   float* scale_out = nullptr; // nullable: the scale used (capture tap)
   int keep_f32 = 0;           // also store every f32 output (capture)
-  int spin_limit = 0;         // barrier polls (~0.2 us each) before a workgroup defers its quantization
+  int spin_limit = 0;         // barrier polls (kBarrierPollUs each) before a workgroup defers its quantization
   int gelu_cert = 1;          // GELU without capture: 1 certified path, 0 exact; 2 and 3 test modes (cert_const)
+  uint32_t* stats = nullptr;  // the context's cumulative barrier counters (kStat*)
 };
 constexpr int64_t kRequantStateBase = 320;
+
+// Cumulative counters of the persistent grids' barriers, one block per
+// program context (handle or worker), never cleared by a run: workgroups
+// that gave up waiting and deferred their quantization to the finisher,
+// workgroups a finisher found unsettled (their tiles were not quantized:
+// the run's result is incomplete and the host reports RGNPU_ERR_DEVICE), and
+// finished barrier launches.
+constexpr int kStatDeferred = 0, kStatUnsettled = 1, kStatLaunches = 2, kStatWords = 4;
+
+// One barrier poll (an s_sleep of 8 x 64 clocks and one agent-scope load of
+// the workgroup's go line), measured on the MI355X with
+// rgnpu_probe_barrier_poll over 256 workgroups: 0.32 us.  The default bound
+// of 100000 polls is therefore ~32 ms before a workgroup defers; a finisher
+// waits at most that plus 100000 polls (~64 ms in all) for a workgroup to
+// settle.
+constexpr double kBarrierPollUs = 0.32;
+// Times `polls` barrier polls of one thread in each of `blocks` workgroups on
+// lines that are never set (requant.hip); returns ms (negative on failure).
+double probe_barrier_poll(uint32_t* lines, int blocks, int polls, hipStream_t s);
 
 // ---- launchers (kernels.hip) -------------------------------------------
 // Launch events: while set_launch_events(events, cap) is active on this
@@ -160,7 +180,8 @@ void launch_gemm_requant(const int8_t* A, const int8_t* B, int64_t M, int64_t N,
 bool input_quant_supported(int64_t M, int64_t K, int64_t Mpad, int64_t Kpad);
 int64_t input_quant_sync_words(int64_t Mpad, int64_t Kpad);
 void launch_input_quant(const float* x, int64_t M, int64_t K, int64_t Mpad, int64_t Kpad, uint32_t* slot, int8_t* q,
-                        float* scale_out, uint32_t* sync, int spin_limit, SlotClear clear, hipStream_t s);
+                        float* scale_out, uint32_t* sync, int spin_limit, uint32_t* stats, SlotClear clear,
+                        hipStream_t s);
 
 // Same contract for M <= 8 rows (weight-streaming GEMV).
 // INT8 Linear with N <= kNarrowMaxN outputs per row: one wave per row, the

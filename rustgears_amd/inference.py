@@ -468,6 +468,14 @@ class InferenceSession:
     def set_profiling(self, level: int) -> None:
         N.check(N.lib().rgnpu_program_set_profiling(self._h, level))
 
+    def barrier_stats(self) -> dict:
+        """Cumulative barrier counters of the persistent grids over this
+        session's contexts (rgnpu_program_barrier_stats): deferred and
+        unsettled workgroups, finished barrier launches."""
+        d, u, l = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+        N.check(N.lib().rgnpu_program_barrier_stats(self._h, ctypes.byref(d), ctypes.byref(u), ctypes.byref(l)))
+        return {"deferred": d.value, "unsettled": u.value, "launches": l.value}
+
     def last_npu_profile(self) -> Optional[NpuProfile]:
         """mod.rs:193-195 (None for the standard FP32 path, which records no
         NPU profile)."""

@@ -89,6 +89,28 @@ def test_every_op_timed_with_four_launch_convs(rg, ref):
     sess.close()
 
 
+def test_fused_pool_records_report_zero_time(rg, ref):
+    """A conv whose 2x2 max pool runs in its epilogue keeps every op's record
+    with the reference's labels; the absorbed pool launches nothing and
+    reports 0 ns, and the conv's record carries the pool's time (its kernel
+    writes the pooled output)."""
+    from rustgears_amd import nn
+    rg.manual_seed(29)
+    layers = (nn.Sequential().add(nn.Conv2d(3, 16, 3).padding(1)).add(nn.Relu()).add(nn.MaxPool2d(2, 2))
+              .add(nn.Flatten()).add(nn.Linear(16 * 16 * 16, 10))).export()
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    x = rg.randn([8, 3, 32, 32])
+    y = sess.run(x)
+    prof = sess.last_npu_profile()
+    assert_bitexact_f32(y, ref.RefProgram(layers).run(x), "int8 conv+pool")
+    labels = [r.op for r in prof.records]
+    assert labels[1] == "NPU::MaxPool2d(k=2)", labels
+    conv, pool = prof.records[0], prof.records[1]
+    assert conv.duration_ns > 0 and conv.kernel_ns > 0, conv
+    assert pool.duration_ns == 0 and pool.kernel_ns == 0, pool
+    sess.close()
+
+
 def test_first_run_of_a_process_is_not_charged_the_code_object_load():
     code = (
         "import sys; sys.path.insert(0, %r)\n"
