@@ -200,6 +200,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ int lds_swz(int r) { return (r >> 1) & 3; }
 
+// Masked stores without branches: raw buffer stores over a wave-uniform
+// base with a record limit of 2^31 bytes; an element outside the output gets
+// the per-lane offset 2^31, which the hardware's bounds check drops, and a
+// row offset can travel in the scalar offset.
+constexpr uint32_t kDropOffset = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kDropOffset, 0x00020000);
+}
+
 // Raw buffer resource over base (gfx9 word 3: 32-bit data format); the
 // record count is left at its maximum, so no store is clipped.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(void* base) {

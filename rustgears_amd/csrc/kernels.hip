@@ -2082,7 +2082,10 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
                                                    const Epilogue& ep, int b, int o0, const int (&pix)[TN / 64],
                                                    float csc, int lane) {
   constexpr int FM = TM / 16, FN = TN / 64;
-  const int64_t O = cs.O, L = cs.OH * cs.OW;
+  const int O = (int)cs.O, L = (int)(cs.OH * cs.OW);
+  // the image's output plane set through a bounded resource: 32-bit offsets
+  // o * L + p (host-checked: O * L * 4 < 2^31), invalid ones dropped
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + (int64_t)b * O * L);
   uint32_t amax = 0;
 #pragma unroll
   for (int i = 0; i < FM; i++)
@@ -2090,17 +2093,18 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
     for (int r = 0; r < 4; r++) {
       const int o = o0 + i * 16 + (lane >> 4) * 4 + r;
       const float bias = ep.bias[o];  // padded to Opad
+      const bool o_ok = o < O;
 #pragma unroll
       for (int j = 0; j < FN; j++) {
         const int p = pix[j];
-        if (o < O && p < L) {
-          const int32_t a = acc[i][j][r];
-          const float v = epi_value<ACT>(a, csc, bias, ep.act_param);
-          ep.y[((int64_t)b * O + o) * L + p] = v;
-          if (ep.acc_out) ep.acc_out[((int64_t)b * L + p) * O + o] = a;
-          const uint32_t key = rgmath::absmax_key(v);
-          amax = key > amax ? key : amax;
-        }
+        const bool ok = o_ok && p < L;
+        const int32_t a = acc[i][j][r];
+        const float v = epi_value<ACT>(a, csc, bias, ep.act_param);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry,
+                                              (int)(ok ? (uint32_t)(o * L + p) * 4u : kDropOffset), 0, 0);
+        if (ep.acc_out && ok) ep.acc_out[((int64_t)b * L + p) * O + o] = a;
+        const uint32_t key = ok ? rgmath::absmax_key(v) : 0u;
+        amax = key > amax ? key : amax;
       }
     }
   if (ep.absmax_out) {
@@ -2128,10 +2132,21 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
                                                          const int (&pix)[TN / 64], float csc, int lane) {
   constexpr int FM = TM / 16, FN = TN / 64;
   static_assert(FN % (2 * R16) == 0, "a wave's pixels are whole pairs of output rows");
-  const int64_t O = cs.O;
+  const int O = (int)cs.O;
   const int OW = (int)cs.OW, L = (int)(cs.OH * cs.OW), POW = OW >> 1;
-  const int64_t PL = (int64_t)(cs.OH >> 1) * POW;
+  const int PL = (int)(cs.OH >> 1) * POW;
   const bool even = (lane & 1) == 0;
+  // the pooled pixel of each even-row fragment (once per lane), stored
+  // through a bounded resource over the image's pooled planes with 32-bit
+  // offsets o * PL + pp (host-checked: O * PL * 4 < 2^31)
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + (int64_t)b * O * PL);
+  int pp[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    const int p = pix[j];
+    const int oy = p / OW, ox = p - oy * OW;
+    pp[j] = (even && p < L) ? (oy >> 1) * POW + (ox >> 1) : -1;
+  }
   uint32_t amax = 0;
 #pragma unroll
   for (int i = 0; i < FM; i++)
@@ -2153,13 +2168,11 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
         best = pool_take(best, h[j]);
         best = pool_take(best, v[jn]);
         best = pool_take(best, h[jn]);
-        const int p = pix[j];
-        if (even && o < O && p < L) {
-          const int oy = p / OW, ox = p - oy * OW;
-          ep.y[((int64_t)b * O + o) * PL + (oy >> 1) * POW + (ox >> 1)] = best;
-          const uint32_t key = rgmath::absmax_key(best);
-          amax = key > amax ? key : amax;
-        }
+        const bool ok = pp[j] >= 0 && o < O;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), ry,
+                                              (int)(ok ? (uint32_t)(o * PL + pp[j]) * 4u : kDropOffset), 0, 0);
+        const uint32_t key = ok ? rgmath::absmax_key(best) : 0u;
+        amax = key > amax ? key : amax;
       }
     }
   if (ep.absmax_out) {
@@ -2180,13 +2193,18 @@ __device__ __forceinline__ void ep_absmax_publish(const uint32_t* slots, int b, 
   const_cast<uint32_t*>(slots)[b] = v;
 }
 
+// CP4 (3- or 4-channel images, the run's first conv) keeps within 128
+// registers, so four of its workgroups share a CU.
 template <int TM, int TN, bool CP4, bool XF = false>
-__global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ Wt,
+__global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_t* __restrict__ xq, const int8_t* __restrict__ Wt,
                                                         ConvShape cs, Epilogue ep, int self_absmax, SlotClear clear) {
   extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
   constexpr int WTN = TN / 4, FM = TM / 16, FN = WTN / 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.z, o0 = blockIdx.y * TM, p0 = blockIdx.x * TN;
+  // grid (images, channel blocks, pixel blocks): the blocks of one image are
+  // dealt to the same XCD (linear workgroup id = image mod 8 for image counts
+  // that are multiples of 8), so they share its L2 for the image's reads
+  const int b = blockIdx.x, o0 = blockIdx.y * TM, p0 = blockIdx.z * TN;
   const int C = (int)cs.C, H = (int)cs.H, W = (int)cs.W, k = (int)cs.k, st = (int)cs.stride, pad = (int)cs.pad;
   const int OW = (int)cs.OW, L = (int)(cs.OH * cs.OW), KP = (int)cs.Kpad, cp = (int)cs.cp, kk = k * k;
   const int wstride = KP + 16, Wp = W + 2 * pad;
@@ -2200,7 +2218,9 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
   // The f32 input's first band batch (see step 2), loaded up front.
   const int iy_base = oy0 * st - pad;
   float img_scale = 0.0f;
-  constexpr int BATCH = 8;
+  // units in flight per thread: with 4 channels (CP4: the run's first conv
+  // of 3-channel images) a band holds few units, fewer registers suffice
+  constexpr int BATCH = CP4 ? 2 : 8;
   float v[BATCH][4];  // unused (and removed) in the i8 form
   int dst[BATCH];
   const float* imgf = reinterpret_cast<const float*>(xq) + (int64_t)b * C * H * W;
@@ -2230,7 +2250,75 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
       *reinterpret_cast<uint32_t*>(band + dst[u]) = word;
     }
   };
-  if constexpr (XF) load_batch(tid);
+  // The vector form of the same fill (rows of a multiple of 4 floats on a
+  // 16-byte boundary): a unit is 4 channels x 4 pixels of one band row, read
+  // with four 16-byte loads through a resource bounded by the image (channels
+  // past C read zeros; rows outside the image get the dropped offset), and
+  // written as four 32-bit LDS words.  A thread's units are 256 apart; their
+  // (channel group, row, pixel quad) advance by the uniform step of 256 units
+  // without divisions.
+  constexpr int B4 = CP4 ? 1 : 4;
+  const bool vec4 = XF && (W & 3) == 0 && (reinterpret_cast<uintptr_t>(xq) & 15) == 0 && C * H * W < (1 << 29);
+  const int wq = W >> 2, per_g4 = R * wq, g4 = cp >> 2, total4 = g4 * per_g4;
+  int ug = 0, ur = 0, ux = 0, sg = 0, sr = 0, sx = 0;
+  if (vec4) {
+    ug = tid / per_g4;
+    const int rem = tid - ug * per_g4;
+    ur = rem / wq;
+    ux = rem - ur * wq;
+    sg = 256 / per_g4;
+    const int srem = 256 - sg * per_g4;
+    sr = srem / wq;
+    sx = srem - sr * wq;
+  }
+  const __amdgpu_buffer_rsrc_t rimg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(imgf), 0, (int)((uint32_t)(C * H * W) * 4u), 0x00020000);
+  v4f w4[B4][4];
+  int d4[B4];
+  auto load4 = [&]() {
+#pragma unroll
+    for (int u = 0; u < B4; u++) {
+      const int iy = iy_base + ur;
+      const bool ok = ug < g4 && iy >= 0 && iy < H;
+      d4[u] = ok ? ((ur * Wp + 4 * ux + pad) * cp + 4 * ug) : -1;
+      const uint32_t off = (uint32_t)(((4 * ug) * H + iy) * W + 4 * ux) * 4u;
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        w4[u][q] = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(rimg, (int)(ok ? off + (uint32_t)(q * H * W) * 4u : kDropOffset),
+                                                       0, 0));
+      ux += sx;
+      if (ux >= wq) {
+        ux -= wq;
+        ur++;
+      }
+      ur += sr;
+      if (ur >= R) {
+        ur -= R;
+        ug++;
+      }
+      ug += sg;
+    }
+  };
+  auto store4 = [&](float inv) {
+#pragma unroll
+    for (int u = 0; u < B4; u++) {
+      if (d4[u] < 0) continue;
+#pragma unroll
+      for (int xx = 0; xx < 4; xx++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) word |= ((uint32_t)rgmath::quantize_rz(w4[u][q][xx] * inv) & 0xffu) << (8 * q);
+        *reinterpret_cast<uint32_t*>(band + d4[u] + xx * cp) = word;
+      }
+    }
+  };
+  if constexpr (XF) {
+    if (vec4)
+      load4();
+    else
+      load_batch(tid);
+  }
 
   // 1. zero the band and the zero block; copy this block's weights.
   for (int i = tid; i <= (band_bytes + 15) / 16; i += 256) *reinterpret_cast<v4i*>(band + 16 * i) = v4i{0, 0, 0, 0};
@@ -2270,16 +2358,24 @@ __global__ __launch_bounds__(256) void conv_band_kernel(const int8_t* __restrict
       if (lane == 0) red[wave] = w;
       __syncthreads();
       const uint32_t t = max(max(red[0], red[1]), max(red[2], red[3]));
-      if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) ep_absmax_publish(ep.absmax_in, b, t);
+      if (tid == 0 && blockIdx.z == 0 && blockIdx.y == 0) ep_absmax_publish(ep.absmax_in, b, t);
       img_scale = rgmath::scale_from_absmax(rgmath::bitsf(t));
     } else {
       img_scale = slot_scale(ep.absmax_in + b);
     }
     const float inv = 1.0f / img_scale;
-    store_batch(inv);
-    for (int e0 = tid + 256 * BATCH; e0 < total; e0 += 256 * BATCH) {
-      load_batch(e0);
+    if (vec4) {
+      store4(inv);
+      for (int e0 = 256 * B4; e0 < total4; e0 += 256 * B4) {
+        load4();
+        store4(inv);
+      }
+    } else {
       store_batch(inv);
+      for (int e0 = tid + 256 * BATCH; e0 < total; e0 += 256 * BATCH) {
+        load_batch(e0);
+        store_batch(inv);
+      }
     }
   } else if ((W & 3) == 0) {
     const int8_t* img = xq + (int64_t)b * C * H * W;
@@ -2482,6 +2578,10 @@ static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& c
                           int self_absmax = 0, SlotClear clear = SlotClear{}) {
   // the fused pool needs whole pairs of output rows per wave (TN / 4 pixels)
   if (ep.pool2 && (!XF || (TN / 4) % (32 * ep.pool2) != 0)) return false;
+  // 32-bit output offsets within one image (o * L + p), pixel blocks in grid.z
+  if (cs.O * cs.OH * cs.OW * 4 >= ((int64_t)1 << 31) || (cs.OH * cs.OW + TN - 1) / TN > 65535 ||
+      cs.n >= ((int64_t)1 << 31))
+    return false;
   const ConvBand g = conv_band_geom(cs, TM, TN);
   constexpr int kStatic = XF ? 64 : 0;  // the f32 form's few words of static LDS
   constexpr int kMaxLds = 160 * 1024 - kStatic;
@@ -2493,7 +2593,7 @@ static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& c
     attr_set = true;
   }
   const int64_t L = cs.OH * cs.OW;
-  dim3 grid((unsigned)((L + TN - 1) / TN), (unsigned)(cs.Opad / TM), (unsigned)cs.n);
+  dim3 grid((unsigned)cs.n, (unsigned)(cs.Opad / TM), (unsigned)((L + TN - 1) / TN));
   RG_LAUNCH((conv_band_kernel<TM, TN, CP4, XF>), grid, dim3(256), (unsigned)g.lds_bytes, s, xq, Wq, cs, ep,
             self_absmax, clear);
   return true;
@@ -2502,6 +2602,12 @@ static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& c
 template <int TM, bool CP4, bool XF>
 static bool try_conv_band_tn(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
                              hipStream_t s, int self_absmax = 0, SlotClear clear = SlotClear{}) {
+  // 256-pixel blocks unless that leaves fewer than two workgroups per CU
+  // (512 on the MI355X's 256 CUs): then 128-pixel blocks first, whose bands
+  // add only their halo rows, so more CUs hold two blocks' latency chains
+  const int64_t L = cs.OH * cs.OW;
+  const bool small_grid = cs.n * (cs.Opad / TM) * ((L + 255) / 256) < 512;
+  if (small_grid && try_conv_band<TM, 128, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear)) return true;
   return try_conv_band<TM, 256, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear) ||
          try_conv_band<TM, 128, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear) ||
          try_conv_band<TM, 64, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear);
@@ -2511,7 +2617,9 @@ bool conv_self_absmax_supported(const ConvShape& cs) { return cs.C * cs.H * cs.W
 
 bool conv_pool_supported(const ConvShape& cs, int r16) {
   if (r16 != 1 && r16 != 2) return false;
-  if (cs.n > 65535 || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31)) return false;
+  if (cs.n >= ((int64_t)1 << 31) || cs.C * cs.H * cs.W >= ((int64_t)1 << 31) || cs.OH * cs.OW >= ((int64_t)1 << 31) ||
+      cs.O * cs.OH * cs.OW * 4 >= ((int64_t)1 << 31) || (cs.OH * cs.OW + 127) / 128 > 65535)
+    return false;
   const int TM = cs.Opad % 64 == 0 ? 64 : 32;
   constexpr int kMaxLds = 160 * 1024 - 64;  // try_conv_band's bound for the f32-input form
   for (const int TN : {256, 128})

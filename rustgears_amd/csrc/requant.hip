@@ -177,16 +177,7 @@ __device__ __forceinline__ uint32_t q8x4(v4f v, float inv) {
   return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-// Masked stores without branches: raw buffer stores over a wave-uniform
-// base with a record limit of 2^31 bytes; an element outside the output gets
-// the per-lane offset 2^31, which the hardware's bounds check drops, and the
-// row offset travels in the scalar offset.
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-constexpr uint32_t kDropOffset = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)kDropOffset, 0x00020000);
-}
 
 // Quantizes 4 values into q's row (byte offset qoff from the wave's q base):
 // rows past M and columns past N are the operand's zero padding.
