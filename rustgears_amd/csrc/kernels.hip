@@ -2077,10 +2077,37 @@ static ConvBand conv_band_geom(const ConvShape& cs, int TM, int TN) {
   return ConvBand{(int)rows, bytes > (1 << 30) ? (1 << 30) : (int)bytes};
 }
 
+// n / d for a divisor d the whole block shares, as a high multiply:
+// mag = ceil(2^32 / d) (div_magic), exact whenever n * d < 2^32.
+__device__ __forceinline__ uint32_t div_magic(uint32_t d) { return d <= 1 ? 0u : 0xffffffffu / d + 1u; }
+__device__ __forceinline__ int udiv(int n, uint32_t mag) { return mag ? (int)__umulhi((uint32_t)n, mag) : n; }
+
+// The block's absmax for the next op: the 4 waves' maxima meet in LDS and
+// one atomic per block raises the image's slot (per image) or one partial of
+// the spread slot (per tensor), so an image slot takes one atomic per block
+// rather than one per wave.  Every thread of the block calls it.
+__device__ __forceinline__ void conv_block_absmax(const Epilogue& ep, int b, uint32_t amax, uint32_t* red, int lane) {
+  if (!ep.absmax_out) return;
+  amax = wave_max_u32(amax);
+  if (lane == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t m = max(max(red[0], red[1]), max(red[2], red[3]));
+    if (m) {
+      if (ep.absmax_out_per_image) {
+        atomicMax(ep.absmax_out + b, m);
+      } else {
+        const uint32_t block = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        atomicMax(ep.absmax_out + (block & (kSpread - 1)) * kSpreadStride, m);
+      }
+    }
+  }
+}
+
 template <int TM, int TN, bool CP4, int ACT>
 __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
                                                    const Epilogue& ep, int b, int o0, const int (&pix)[TN / 64],
-                                                   float csc, int lane) {
+                                                   float csc, int lane, uint32_t* red) {
   constexpr int FM = TM / 16, FN = TN / 64;
   const int O = (int)cs.O, L = (int)(cs.OH * cs.OW);
   // the image's output plane set through a bounded resource: 32-bit offsets
@@ -2107,14 +2134,7 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
         amax = key > amax ? key : amax;
       }
     }
-  if (ep.absmax_out) {
-    amax = wave_max_u32(amax);
-    if (ep.absmax_out_per_image) {
-      if (lane == 0 && amax) atomicMax(ep.absmax_out + b, amax);
-    } else if (lane == 0) {
-      spread_max(ep.absmax_out, amax);
-    }
-  }
+  conv_block_absmax(ep, b, amax, red, lane);
 }
 
 // Conv -> MaxPool2d(2, 2) (npu.rs:384-390 on the output of npu.rs:319-383)
@@ -2129,7 +2149,8 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
 template <int TM, int TN, int ACT, int R16>
 __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
                                                          const Epilogue& ep, int b, int o0,
-                                                         const int (&pix)[TN / 64], float csc, int lane) {
+                                                         const int (&pix)[TN / 64], float csc, int lane,
+                                                         uint32_t* red) {
   constexpr int FM = TM / 16, FN = TN / 64;
   static_assert(FN % (2 * R16) == 0, "a wave's pixels are whole pairs of output rows");
   const int O = (int)cs.O;
@@ -2140,11 +2161,15 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
   // through a bounded resource over the image's pooled planes with 32-bit
   // offsets o * PL + pp (host-checked: O * PL * 4 < 2^31)
   const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + (int64_t)b * O * PL);
+  float4 b4[FM];  // the lane's 4 output channels of each row block (bias padded to Opad)
+#pragma unroll
+  for (int i = 0; i < FM; i++) b4[i] = *reinterpret_cast<const float4*>(ep.bias + o0 + i * 16 + (lane >> 4) * 4);
   int pp[FN];
+  const uint32_t owmag = div_magic((uint32_t)OW);
 #pragma unroll
   for (int j = 0; j < FN; j++) {
     const int p = pix[j];
-    const int oy = p / OW, ox = p - oy * OW;
+    const int oy = udiv(p, owmag), ox = p - oy * OW;
     pp[j] = (even && p < L) ? (oy >> 1) * POW + (ox >> 1) : -1;
   }
   uint32_t amax = 0;
@@ -2153,7 +2178,7 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int o = o0 + i * 16 + (lane >> 4) * 4 + r;
-      const float bias = ep.bias[o];  // padded to Opad
+      const float bias = b4[i][r];  // padded to Opad
       float v[FN], h[FN];
 #pragma unroll
       for (int j = 0; j < FN; j++) v[j] = epi_value<ACT>(acc[i][j][r], csc, bias, ep.act_param);
@@ -2163,26 +2188,25 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
       for (int j = 0; j < FN; j++) {
         if ((j / R16) % 2 != 0) continue;
         const int jn = j + R16 < FN ? j + R16 : j;  // j + R16 whenever j's row is even
-        float best = -__builtin_inff();
-        best = pool_take(best, v[j]);
-        best = pool_take(best, h[j]);
-        best = pool_take(best, v[jn]);
-        best = pool_take(best, h[jn]);
+        float best;
+        if constexpr (ACT == rgmath::ACT_RELU) {
+          // ReLU leaves no NaN and no -0 (x > 0 ? x : +0), so pool_take's
+          // first-maximum rule is the plain maximum of the four values
+          best = __builtin_fmaxf(__builtin_fmaxf(v[j], h[j]), __builtin_fmaxf(v[jn], h[jn]));
+        } else {
+          best = v[j];  // pool_take(-inf, v) == v for every v
+          best = pool_take(best, h[j]);
+          best = pool_take(best, v[jn]);
+          best = pool_take(best, h[jn]);
+        }
         const bool ok = pp[j] >= 0 && o < O;
         __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), ry,
                                               (int)(ok ? (uint32_t)(o * PL + pp[j]) * 4u : kDropOffset), 0, 0);
-        const uint32_t key = ok ? rgmath::absmax_key(best) : 0u;
+        const uint32_t key = ok ? (ACT == rgmath::ACT_RELU ? rgmath::fbits(best) : rgmath::absmax_key(best)) : 0u;
         amax = key > amax ? key : amax;
       }
     }
-  if (ep.absmax_out) {
-    amax = wave_max_u32(amax);
-    if (ep.absmax_out_per_image) {
-      if (lane == 0 && amax) atomicMax(ep.absmax_out + b, amax);
-    } else if (lane == 0) {
-      spread_max(ep.absmax_out, amax);
-    }
-  }
+  conv_block_absmax(ep, b, amax, red, lane);
 }
 
 constexpr int64_t kConvSelfAbsmaxMax = 16384;
@@ -2313,7 +2337,23 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
       }
     }
   };
+  // The image's absmax comes first: with self_absmax the first 4 x 256
+  // 16-byte pieces of the image, else the image's slot, are loaded before the
+  // band and the weights, so all three share one memory round trip.
+  __shared__ uint32_t red[4];
+  const int n_img = C * H * W;
+  const bool am_vec = XF && self_absmax && (n_img & 3) == 0 && (reinterpret_cast<uintptr_t>(imgf) & 15) == 0;
+  float4 am4[4];
+  uint32_t slot_bits = 0;
   if constexpr (XF) {
+    if (am_vec) {
+      const float4* f4 = reinterpret_cast<const float4*>(imgf);
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        am4[u] = tid + u * 256 < (n_img >> 2) ? f4[tid + u * 256] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    } else if (!self_absmax) {
+      slot_bits = ep.absmax_in[b];
+    }
     if (vec4)
       load4();
     else
@@ -2323,8 +2363,9 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
   // 1. zero the band and the zero block; copy this block's weights.
   for (int i = tid; i <= (band_bytes + 15) / 16; i += 256) *reinterpret_cast<v4i*>(band + 16 * i) = v4i{0, 0, 0, 0};
   const int kc = KP / 16;
+  const uint32_t kcmag = div_magic((uint32_t)kc);
   for (int i = tid; i < TM * kc; i += 256) {
-    const int row = i / kc, c16 = i - row * kc;
+    const int row = udiv(i, kcmag), c16 = i - row * kc;
     *reinterpret_cast<v4i*>(wts + row * wstride + c16 * 16) =
         *reinterpret_cast<const v4i*>(Wt + (int64_t)(o0 + row) * KP + c16 * 16);
   }
@@ -2336,32 +2377,32 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
     if (self_absmax) {
       clear_slots(clear);
       float m = 0.0f;  // NaN ignored, like f32::max
-      const int n = C * H * W;
-      if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(imgf) & 15) == 0) {
+      if (am_vec) {
         const float4* f4 = reinterpret_cast<const float4*>(imgf);
-        const int n4 = n >> 2;
-        for (int e = tid; e < n4; e += 4 * 256) {
-          float4 w4[4];
-#pragma unroll
-          for (int u = 0; u < 4; u++) w4[u] = e + u * 256 < n4 ? f4[e + u * 256] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        const int n4 = n_img >> 2;
+        for (int e = tid;; e += 4 * 256) {
 #pragma unroll
           for (int u = 0; u < 4; u++) {
-            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(w4[u].x)), __builtin_fabsf(w4[u].y));
-            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(w4[u].z)), __builtin_fabsf(w4[u].w));
+            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(am4[u].x)), __builtin_fabsf(am4[u].y));
+            m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(am4[u].z)), __builtin_fabsf(am4[u].w));
           }
+          if (e + 4 * 256 >= n4) break;
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+            am4[u] = e + 4 * 256 + u * 256 < n4 ? f4[e + 4 * 256 + u * 256] : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
       } else {
-        for (int e = tid; e < n; e += 256) m = __builtin_fmaxf(m, __builtin_fabsf(imgf[e]));
+        for (int e = tid; e < n_img; e += 256) m = __builtin_fmaxf(m, __builtin_fabsf(imgf[e]));
       }
-      __shared__ uint32_t red[4];
       const uint32_t w = wave_max_u32(rgmath::fbits(m));
       if (lane == 0) red[wave] = w;
       __syncthreads();
       const uint32_t t = max(max(red[0], red[1]), max(red[2], red[3]));
       if (tid == 0 && blockIdx.z == 0 && blockIdx.y == 0) ep_absmax_publish(ep.absmax_in, b, t);
       img_scale = rgmath::scale_from_absmax(rgmath::bitsf(t));
+      __syncthreads();  // red is reused by the epilogue's absmax
     } else {
-      img_scale = slot_scale(ep.absmax_in + b);
+      img_scale = rgmath::scale_from_absmax(rgmath::bitsf(slot_bits));
     }
     const float inv = 1.0f / img_scale;
     if (vec4) {
@@ -2404,11 +2445,12 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
   __syncthreads();
 
   // 3. per-lane pixels and the byte offset of their tap (0, 0), channel 0.
+  const uint32_t owmag_k = div_magic((uint32_t)OW), kmag = div_magic((uint32_t)k), cpmag = div_magic((uint32_t)cp);
   int pix[FN], rowoff[FN];
 #pragma unroll
   for (int j = 0; j < FN; j++) {
     pix[j] = p0 + wave * WTN + j * 16 + (lane & 15);
-    const int oy = pix[j] / OW, ox = pix[j] - oy * OW;
+    const int oy = udiv(pix[j], owmag_k), ox = pix[j] - oy * OW;
     rowoff[j] = pix[j] < L ? ((oy - oy0) * st * Wp + ox * st) * cp : -1;
   }
   v4i acc[FM][FN];
@@ -2422,8 +2464,8 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
 #pragma unroll
     for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(wts + (i * 16 + (lane & 15)) * wstride + kb);
     if (!CP4) {
-      const int tap = kb / cp, c0 = kb - tap * cp;
-      const int ki = tap / k, kj = tap - ki * k;
+      const int tap = udiv(kb, cpmag), c0 = kb - tap * cp;
+      const int ki = udiv(tap, kmag), kj = tap - ki * k;
       const int toff = (ki * Wp + kj) * cp + c0;
 #pragma unroll
       for (int j = 0; j < FN; j++) {
@@ -2434,7 +2476,7 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int tap = (kb >> 2) + e;
-        const int ki = tap / k, kj = tap - ki * k;
+        const int ki = udiv(tap, kmag), kj = tap - ki * k;
         const int toff = (ki * Wp + kj) * 4;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
@@ -2460,26 +2502,26 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
       const bool relu = ep.act == rgmath::ACT_RELU;
       if constexpr (TN / 64 >= 4) {
         if (ep.pool2 == 2) {
-          relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 2>(acc, cs, ep, b, o0, pix, csc, lane)
-               : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 2>(acc, cs, ep, b, o0, pix, csc, lane);
+          relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 2>(acc, cs, ep, b, o0, pix, csc, lane, red)
+               : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 2>(acc, cs, ep, b, o0, pix, csc, lane, red);
           return;
         }
       }
-      relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 1>(acc, cs, ep, b, o0, pix, csc, lane)
-           : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 1>(acc, cs, ep, b, o0, pix, csc, lane);
+      relu ? conv_band_epilogue_pool2<TM, TN, rgmath::ACT_RELU, 1>(acc, cs, ep, b, o0, pix, csc, lane, red)
+           : conv_band_epilogue_pool2<TM, TN, rgmath::ACT_NONE, 1>(acc, cs, ep, b, o0, pix, csc, lane, red);
       return;
     }
   }
   switch (ep.act) {
-    case rgmath::ACT_RELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_RELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
-    case rgmath::ACT_SIGMOID: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SIGMOID>(acc, cs, ep, b, o0, pix, csc, lane); break;
-    case rgmath::ACT_TANH: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_TANH>(acc, cs, ep, b, o0, pix, csc, lane); break;
-    case rgmath::ACT_GELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_GELU>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_RELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_RELU>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
+    case rgmath::ACT_SIGMOID: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SIGMOID>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
+    case rgmath::ACT_TANH: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_TANH>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
+    case rgmath::ACT_GELU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_GELU>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
     case rgmath::ACT_LEAKY_RELU:
-      conv_band_epilogue<TM, TN, CP4, rgmath::ACT_LEAKY_RELU>(acc, cs, ep, b, o0, pix, csc, lane);
+      conv_band_epilogue<TM, TN, CP4, rgmath::ACT_LEAKY_RELU>(acc, cs, ep, b, o0, pix, csc, lane, red);
       break;
-    case rgmath::ACT_SILU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SILU>(acc, cs, ep, b, o0, pix, csc, lane); break;
-    default: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_NONE>(acc, cs, ep, b, o0, pix, csc, lane); break;
+    case rgmath::ACT_SILU: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_SILU>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
+    default: conv_band_epilogue<TM, TN, CP4, rgmath::ACT_NONE>(acc, cs, ep, b, o0, pix, csc, lane, red); break;
   }
 }
 
@@ -2573,9 +2615,18 @@ __global__ __launch_bounds__(256) void conv_i8_kernel(const int8_t* __restrict__
   epilogue_tile<TM, TN, CLD, true>(Cs, tc, csc, ep);
 }
 
+// The band kernel divides by the block's shape with high multiplies
+// (div_magic), exact when dividend x divisor < 2^32: pixels by OW, taps by k,
+// K bytes by cp, weight chunks by Kpad / 16.
+static bool conv_band_indexable(const ConvShape& cs, int TM, int TN) {
+  const int64_t lim = (int64_t)1 << 32, L = cs.OH * cs.OW, kc = cs.Kpad / 16;
+  return (L + TN) * cs.OW < lim && (cs.Kpad / 4 + 4) * cs.k < lim && cs.Kpad * cs.cp < lim && (TM * kc + 256) * kc < lim;
+}
+
 template <int TM, int TN, bool CP4, bool XF>
 static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s,
                           int self_absmax = 0, SlotClear clear = SlotClear{}) {
+  if (!conv_band_indexable(cs, TM, TN)) return false;
   // the fused pool needs whole pairs of output rows per wave (TN / 4 pixels)
   if (ep.pool2 && (!XF || (TN / 4) % (32 * ep.pool2) != 0)) return false;
   // 32-bit output offsets within one image (o * L + p), pixel blocks in grid.z
@@ -2583,7 +2634,7 @@ static bool try_conv_band(const int8_t* xq, const int8_t* Wq, const ConvShape& c
       cs.n >= ((int64_t)1 << 31))
     return false;
   const ConvBand g = conv_band_geom(cs, TM, TN);
-  constexpr int kStatic = XF ? 64 : 0;  // the f32 form's few words of static LDS
+  constexpr int kStatic = 64;  // the kernel's few words of static LDS
   constexpr int kMaxLds = 160 * 1024 - kStatic;
   if (g.lds_bytes > kMaxLds) return false;
   const void* fn = reinterpret_cast<const void*>(&conv_band_kernel<TM, TN, CP4, XF>);
@@ -2623,7 +2674,8 @@ bool conv_pool_supported(const ConvShape& cs, int r16) {
   const int TM = cs.Opad % 64 == 0 ? 64 : 32;
   constexpr int kMaxLds = 160 * 1024 - 64;  // try_conv_band's bound for the f32-input form
   for (const int TN : {256, 128})
-    if ((TN / 4) % (32 * r16) == 0 && conv_band_geom(cs, TM, TN).lds_bytes <= kMaxLds) return true;
+    if ((TN / 4) % (32 * r16) == 0 && conv_band_geom(cs, TM, TN).lds_bytes <= kMaxLds && conv_band_indexable(cs, TM, TN))
+      return true;
   return false;
 }
 
