@@ -2183,7 +2183,7 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
 #pragma unroll
       for (int j = 0; j < FN; j++) v[j] = epi_value<ACT>(acc[i][j][r], csc, bias, ep.act_param);
 #pragma unroll
-      for (int j = 0; j < FN; j++) h[j] = __shfl_xor(v[j], 1);
+      for (int j = 0; j < FN; j++) h[j] = __int_as_float(dpp_partner<1>(__float_as_int(v[j])));  // lane ^ 1
 #pragma unroll
       for (int j = 0; j < FN; j++) {
         if ((j / R16) % 2 != 0) continue;
@@ -2264,14 +2264,21 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
       }
     }
   };
+  // The image's scale comes from its own absmax (over every pixel a window
+  // reads), so the clamp cannot act on those pixels (quantize_rz_bounded);
+  // pixels no window reads are never used.  Four bytes pack with v_perm.
+  auto pack4b = [](float a, float b_, float c, float d, float inv) -> uint32_t {
+    const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(a * inv), b1 = (uint32_t)rgmath::quantize_rz_bounded(b_ * inv);
+    const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(c * inv), b3 = (uint32_t)rgmath::quantize_rz_bounded(d * inv);
+    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // bytes b0.0, b1.0
+    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  };
   auto store_batch = [&](float inv) {
 #pragma unroll
     for (int u = 0; u < BATCH; u++) {
       if (dst[u] < 0) continue;
-      uint32_t word = 0;
-#pragma unroll
-      for (int q = 0; q < 4; q++) word |= ((uint32_t)rgmath::quantize_rz(v[u][q] * inv) & 0xffu) << (8 * q);
-      *reinterpret_cast<uint32_t*>(band + dst[u]) = word;
+      *reinterpret_cast<uint32_t*>(band + dst[u]) = pack4b(v[u][0], v[u][1], v[u][2], v[u][3], inv);
     }
   };
   // The vector form of the same fill (rows of a multiple of 4 floats on a
@@ -2329,12 +2336,9 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
     for (int u = 0; u < B4; u++) {
       if (d4[u] < 0) continue;
 #pragma unroll
-      for (int xx = 0; xx < 4; xx++) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) word |= ((uint32_t)rgmath::quantize_rz(w4[u][q][xx] * inv) & 0xffu) << (8 * q);
-        *reinterpret_cast<uint32_t*>(band + d4[u] + xx * cp) = word;
-      }
+      for (int xx = 0; xx < 4; xx++)
+        *reinterpret_cast<uint32_t*>(band + d4[u] + xx * cp) =
+            pack4b(w4[u][0][xx], w4[u][1][xx], w4[u][2][xx], w4[u][3][xx], inv);
     }
   };
   // The image's absmax comes first: with self_absmax the first 4 x 256
@@ -2657,6 +2661,14 @@ static bool try_conv_band_tn(const int8_t* xq, const int8_t* Wq, const ConvShape
   // (512 on the MI355X's 256 CUs): then 128-pixel blocks first, whose bands
   // add only their halo rows, so more CUs hold two blocks' latency chains
   const int64_t L = cs.OH * cs.OW;
+  // RGNPU_CONV_TN (64, 128 or 256) tries that block width first (measurement aid)
+  static const int forced = [] {
+    const char* e = getenv("RGNPU_CONV_TN");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced == 64 && try_conv_band<TM, 64, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear)) return true;
+  if (forced == 128 && try_conv_band<TM, 128, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear)) return true;
+  if (forced == 256 && try_conv_band<TM, 256, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear)) return true;
   const bool small_grid = cs.n * (cs.Opad / TM) * ((L + 255) / 256) < 512;
   if (small_grid && try_conv_band<TM, 128, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear)) return true;
   return try_conv_band<TM, 256, CP4, XF>(xq, Wq, cs, ep, s, self_absmax, clear) ||
