@@ -162,6 +162,7 @@ struct OpPlan {
 struct Plan {
   std::vector<int64_t> in_shape, out_shape;
   bool capture = false;  // made for capture runs (no conv-pool fusion)
+  bool persistent = true;  // may launch persistent grids (fused requantization, one-pass input quantization)
   int64_t in_len = 0, out_len = 0;
   std::vector<OpPlan> ops;
   size_t f32_elems = 0, q_bytes = 0, ylo_elems = 0;
@@ -245,6 +246,14 @@ struct rgnpu_program {
   DevBuf stats;
   uint32_t* stats_host = nullptr;
   uint32_t unsettled_seen = 0;
+  // Whether this context's next run may use persistent grids (make_plan):
+  // the handle's runs always; a worker's runs until the program has once had
+  // two host runs in flight together (concurrent_seen, set by the handle
+  // and sticky).  The plan of the other kind is kept in plan_other, so a
+  // change of kind does not rebuild plans.
+  bool use_persistent = true;
+  bool concurrent_seen = false;
+  std::unique_ptr<Plan> plan_other;
 };
 
 // Bytes read between benchmark runs to displace the 256 MB memory-side cache.
@@ -856,8 +865,20 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   // unsplit MFMA GEMM whose next computing op is a Linear reading the same
   // rows (its absmax is this op's emitted slot).  Its barrier words join the
   // slot set, which every run zeroes.
+  //
+  // Persistent grids (this fusion and the one-pass input quantization below)
+  // take every resident workgroup slot and meet at a grid barrier, so they
+  // need the whole GPU to themselves.  Host-pointer runs of several threads
+  // run on worker streams at once, and there the other streams' kernels
+  // (GEMMs, copies) keep taking the slots such a grid waits for: its
+  // workgroups then wait out the barrier's bound (~32 ms) and defer.  Once
+  // two host runs of a program have overlapped, its worker runs therefore use
+  // plans with the separate quantize kernels (the same arithmetic); those
+  // runs are bound by their host copies anyway.
+  const bool persistent_ok = P->use_persistent;
+  plan->persistent = persistent_ok;
   bool any_requant = false;
-  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8 && persistent_ok; i++) {
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR || pl.gemv || op.out_f <= kNarrowMaxN || pl.rows <= 0 || op.out_f % 4) continue;
@@ -905,7 +926,7 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   }
   // A Linear that quantizes its own input does so in one pass when the
   // shapes fit the kernel's 32-bit offsets.
-  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8; i++) {
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8 && persistent_ok; i++) {
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR || !pl.explicit_absmax || pl.rows <= 0 ||
@@ -1060,13 +1081,24 @@ static void read_stats(rgnpu_program* P) {
   RG_HIP(hipStreamSynchronize(P->stream));
 }
 
+static bool plan_fits(const Plan* pl, const rgnpu_program* P, const int64_t* shape, int ndim) {
+  return pl && (int)pl->in_shape.size() == ndim && pl->capture == P->capture &&
+         pl->persistent == P->use_persistent && std::equal(pl->in_shape.begin(), pl->in_shape.end(), shape);
+}
+
 static Plan& get_plan(rgnpu_program* P, const int64_t* shape, int ndim) {
-  if (P->plan && (int)P->plan->in_shape.size() == ndim && P->plan->capture == P->capture &&
-      std::equal(P->plan->in_shape.begin(), P->plan->in_shape.end(), shape))
-    return *P->plan;
+  if (plan_fits(P->plan.get(), P, shape, ndim)) return *P->plan;
   // A pending profile reads the roles and events of the plan it ran with:
-  // settle it before that plan goes away.
+  // settle it before that plan stops being the current one.
   if (P->plan && P->profile_pending) finalize_profile(P);
+  if (plan_fits(P->plan_other.get(), P, shape, ndim)) {
+    std::swap(P->plan, P->plan_other);
+    return *P->plan;
+  }
+  // keep the current plan as the other kind when only the kind changes
+  const bool same_shape = P->plan && (int)P->plan->in_shape.size() == ndim && P->plan->capture == P->capture &&
+                          std::equal(P->plan->in_shape.begin(), P->plan->in_shape.end(), shape);
+  P->plan_other = same_shape ? std::move(P->plan) : nullptr;
   P->plan.reset();
   P->plan = make_plan(P, shape, ndim);
   return *P->plan;
@@ -1686,6 +1718,14 @@ int rgnpu_program_run(rgnpu_program* P, const float* x, const int64_t* shape, in
     ~Release() { release_worker(P, W); }
   } rel{P, W};
   W->profiling = profiling;
+  {
+    // persistent grids until two host runs of this program have overlapped
+    std::lock_guard<std::mutex> lk(P->pool_mu);
+    int busy = 0;
+    for (char b : P->worker_busy) busy += b != 0;
+    if (busy > 1) P->concurrent_seen = true;
+    W->use_persistent = !P->concurrent_seen;
+  }
   run_host(W, x, shape, ndim, y, y_cap, y_shape, y_ndim);
   if (y && W->have_profile) {
     // the last completed run's profile (mod.rs:217)

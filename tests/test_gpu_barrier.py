@@ -6,8 +6,9 @@ quantization): its counters and the cost of one poll.
 * With RGNPU_REQUANT_SPIN_LIMIT=0 every workgroup but the finisher defers,
   the results stay bit-exact, and nothing is unsettled.
 * Runs from several host threads on one session (worker streams, each with
-  its own grids) stay bit-identical to the serial result; the deferrals they
-  cause are counted and printed.
+  its own grids that each fill the GPU) stay bit-identical to the serial
+  result, and none of their workgroups defers: worker streams order their
+  persistent grids.
 * One poll's cost (rgnpu_probe_barrier_poll) is what the wait bound's
   documentation states (kBarrierPollUs).
 """
@@ -62,31 +63,43 @@ def test_barrier_counters_with_forced_deferral(rg, ref, monkeypatch):
 
 
 def test_barrier_counters_under_concurrent_runs(rg, ref):
-    layers, x = _stack(rg)
+    """8192 rows of 2048-wide layers: 256 tiles of 256 x 256, so every
+    persistent grid asks for the whole GPU.  Once two host runs of a session
+    have overlapped, its worker runs use the plans without persistent grids
+    (program.cpp make_plan), so after a first concurrent round nothing
+    launches a barrier grid and nothing defers; every output stays
+    bit-identical to the serial result."""
+    layers, x = _stack(rg, rows=8192)
     want = ref.RefProgram(layers).run(x, parallel=True)
     sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
     errors = []
 
-    def worker(k):
+    def rounds(k, n):
         try:
-            for _ in range(6):
+            for _ in range(n):
                 y = sess.run(x)
                 if not np.array_equal(y.view(np.uint32), want.view(np.uint32)):
                     errors.append(f"thread {k}: output differs")
         except Exception as e:  # noqa: BLE001 -- reported below
             errors.append(f"thread {k}: {e}")
 
-    print("[barrier] 4 threads x 6 runs on one session", flush=True)
-    ts = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
-    for t in ts:
-        t.start()
-    for t in ts:
-        t.join()
+    def threads(n):
+        ts = [threading.Thread(target=rounds, args=(k, n)) for k in range(4)]
+        for t in ts:
+            t.start()
+        for t in ts:
+            t.join()
+
+    print("[barrier] 4 threads x 2 runs, then 4 threads x 6 runs on one session", flush=True)
+    threads(2)
+    first = sess.barrier_stats()
+    threads(6)
     st = sess.barrier_stats()
     sess.close()
     assert not errors, errors
-    assert st["unsettled"] == 0 and st["launches"] == 3 * 24, st
-    print(f"[barrier] concurrent: {st}", flush=True)
+    assert st["unsettled"] == 0, st
+    assert st["launches"] == first["launches"] and st["deferred"] == first["deferred"], (first, st)
+    print(f"[barrier] concurrent: first round {first}, after {st}", flush=True)
 
 
 def test_barrier_poll_cost(rg):
