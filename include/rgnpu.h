@@ -146,8 +146,10 @@ int rgnpu_program_synchronize(rgnpu_program* prog);
 
 /* Allocation-free variant of rgnpu_program_run_device, with the same
  * arguments and results.  No counterpart in the reference: it is for callers
- * that cannot allocate device memory (code under HIP graph capture, serving
- * loops and harnesses that forbid hipMalloc).  The call makes no hipMalloc or
+ * that cannot allocate device memory (serving loops and harnesses that forbid
+ * hipMalloc).  It allocates no device memory but is not capture-safe: every
+ * call uploads the conv programs' coverage masks from host memory the plan
+ * owns, and a new input shape synchronizes the stream.  The call makes no hipMalloc or
  * hipFree: every intermediate buffer of the run (activations between ops,
  * the i8 / binary16 GEMM operands, absmax slots, scales, conv coverage
  * masks, split-K partial sums) is a view into one device array of
