@@ -11,6 +11,8 @@
 //   mfma+barrier     + the workgroup barrier of every K step
 //   mfma+barrier+lds + the step's 12 fragment reads from LDS (ring stages
 //                    rotated, no DMA)
+//   mfma32*          the three above with v_mfma_i32_32x32x32_i8 (16 MFMAs
+//                    per step, the same wave tile and fragment reads)
 //   production/4     gemm_core.h big_kloop, the 4-stage DMA ring of the
 //                    product's 256 x 256 GEMM, on random A [8192, 4096] and
 //                    B [4096, 4096]
@@ -36,6 +38,7 @@ namespace rgnpu {
 hipEvent_t next_launch_event() { return nullptr; }
 }  // namespace rgnpu
 using namespace rgnpu;
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 #define CK(e)                                                                             \
   do {                                                                                    \
@@ -106,6 +109,79 @@ __global__ __launch_bounds__(512, 1) void reg_loop(const int32_t* __restrict__ s
     for (int j = 0; j < 4; j++) x ^= acc[i][j][0] ^ acc[i][j][1] ^ acc[i][j][2] ^ acc[i][j][3];
 #pragma unroll
   for (int c = 0; c < 8; c++) x ^= __float_as_int(f[c]);
+  if (x == never) sink[0] = x;
+}
+
+// The register-only variants with v_mfma_i32_32x32x32_i8: the same 128 x 64
+// wave tile as 4 x 2 blocks of 32 x 32, each K step of 64 bytes as two
+// halves, so 16 MFMAs of twice the work per step (the same 274.9 G ops) and,
+// with MODE 2, the same 12 fragment reads of 16 bytes per lane (lane l reads
+// row l % 32 of its block, K bytes 32 h + 16 (l / 32) of the half h).
+template <int MODE>
+__global__ __launch_bounds__(512, 1) void reg_loop32(const int32_t* __restrict__ seed, int32_t never,
+                                                     int32_t* __restrict__ sink) {
+  __shared__ __attribute__((aligned(1024))) int8_t smem[4 * 32768];
+  const int l = threadIdx.x, lane = l & 63, wave = l >> 6;
+  for (int i = l; i < 4 * 32768 / 4; i += 512) reinterpret_cast<int32_t*>(smem)[i] = seed[i & 255] ^ (i * 0x9e3779b9);
+  __syncthreads();
+  v4i a[4][2], b[2][2];
+  v16i acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      a[i][h] = v4i{seed[(l + 2 * i + h) & 255], seed[(l + 3 * i + 1) & 255], seed[(l + 5 * i + h + 2) & 255],
+                    seed[(l + 7 * i + 3) & 255]};
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+      b[j][h] = v4i{seed[(l + 11 * j + h) & 255], seed[(l + 13 * j + 5) & 255], seed[(l + 17 * j + h + 6) & 255],
+                    seed[(l + 19 * j + 7) & 255]};
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0;
+  const int wm = wave / 4, wn = wave % 4;
+  const int row = lane & 31;
+  uint32_t rdh[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++)
+    rdh[h] = (uint32_t)(row * 64 + (((2 * h + (lane >> 5)) ^ lds_swz(row & 15)) << 4));
+  uint32_t st = 0;
+  for (int it = 0; it < 2 * kSteps; it++) {  // 2 tiles per workgroup
+    if constexpr (MODE >= 1) {
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+    if constexpr (MODE == 2) {
+      const int8_t* sa = smem + st;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          b[j][h] = *reinterpret_cast<const v4i*>(sa + 16384 + (wn * 64 + j * 32) * 64 + rdh[h]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) a[i][h] = *reinterpret_cast<const v4i*>(sa + (wm * 128 + i * 32) * 64 + rdh[h]);
+      }
+      st = st == 3 * 32768 ? 0 : st + 32768;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i][h], b[j][h], acc[i][j], 0, 0, 0);
+  }
+  int32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) x ^= acc[i][j][e];
   if (x == never) sink[0] = x;
 }
 
@@ -253,6 +329,9 @@ int main(int argc, char** argv) {
   report("mfma", median_ms([&] { hipLaunchKernelGGL((reg_loop<0, 0>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
   report("mfma+barrier", median_ms([&] { hipLaunchKernelGGL((reg_loop<1, 0>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
   report("mfma+barrier+lds", median_ms([&] { hipLaunchKernelGGL((reg_loop<2, 0>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
+  report("mfma32", median_ms([&] { hipLaunchKernelGGL((reg_loop32<0>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
+  report("mfma32+barrier", median_ms([&] { hipLaunchKernelGGL((reg_loop32<1>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
+  report("mfma32+barrier+lds", median_ms([&] { hipLaunchKernelGGL((reg_loop32<2>), dim3(kBlocks), dim3(512), 0, 0, seed, never, sink); }, reps));
   report("production/4", median_ms([&] { hipLaunchKernelGGL((ring_loop<4>), dim3(kBlocks), dim3(512), 0, 0, A, B, never, sink); }, reps));
   report("production/3", median_ms([&] { hipLaunchKernelGGL((ring_loop<3>), dim3(kBlocks), dim3(512), 0, 0, A, B, never, sink); }, reps));
   report("wide/lds", median_ms([&] { hipLaunchKernelGGL((wide_loop<false>), dim3(kBlocks), dim3(256), 0, 0, seed, never, sink); }, reps));
