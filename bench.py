@@ -261,6 +261,9 @@ def main():
                     help="activation of the linear_stack workload (gelu is the benchmark config)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--device-only", action="store_true",
+                    help="skip the host-pointer rates (pcie_inclusive*): profiler runs of the device-resident "
+                         "region")
     ap.add_argument("--precision", default="int8", choices=["int8", "fp16", "fp32"],
                     help="NpuPrecision of the session (the headline metric is INT8)")
     args = ap.parse_args()
@@ -347,6 +350,12 @@ def main():
             n += 1
         return n
 
+    if args.device_only:
+        if not args.no_cpu_baseline:
+            line["cpu_baseline"] = cpu_baseline(args.workload, layers, x, args.cpu_seconds, args.precision)
+            line["cpu_baseline"]["host"] = host_description()
+        print(json.dumps(line), flush=True)
+        return
     sess.run(x)
     h0 = time.perf_counter()
     n_host = host_runs(h0 + HOST_S)

@@ -2010,6 +2010,205 @@ void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N
   launch_gemm_narrow_t<kModeI8, true>(reinterpret_cast<const int8_t*>(x), B, M, N, Kpad, ep, s, K, q_out, scale_out);
 }
 
+// ---------------------------------------------------------------------------
+// A whole program of small INT8 Linears in one workgroup (npu.rs:307-318 op
+// after op).  The input, every layer's weights and biases are copied into LDS
+// by global_load_lds (every copy in flight at once, one memory round trip).
+// Each layer then
+//  * folds its input's absmax with absmax_key (NaN ignored, as absmax_kernel
+//    and the producing epilogues do) and takes scale_from_absmax of it
+//    (quantize.rs:19-21);
+//  * quantizes the input with quantize_one into an i8 operand [rows, Kpad]
+//    with zero padding, the rule of quant_rows_kernel (quantize.rs:22);
+//  * forms each exact i32 sum with v_dot4_i32_i8 and applies the fused
+//    epilogue epi_value, fl(fl(float(acc) * fl(scale * w_scale)) + b) and the
+//    activation (quantize.rs:104-113), into the other activation buffer or,
+//    for the last layer, into y.
+// The arithmetic is that of the per-op kernels, so the output is the same bit
+// for bit; what goes is the launches between the ops, which are most of the
+// time of a program this small.
+// ---------------------------------------------------------------------------
+namespace tiny {
+constexpr int kThreads = 1024;  // 4 waves per SIMD of the one CU: they hide each other's LDS latency
+// LDS row strides: f32 activations odd (a wave's lanes store one column of
+// consecutive rows without bank conflicts), the i8 operand 16 bytes past
+// Kpad (16 consecutive rows start in 16 different 4-bank groups)
+constexpr int kActLd = kTinyWidth + 1;
+constexpr int kActWords = kTinyRows * kActLd;
+constexpr int kQaLd = kTinyWidth + 16;
+constexpr int kBiasWords = kTinyMaxLayers * kTinyWidth;
+}  // namespace tiny
+
+// One global_load_lds_dword: 4 bytes per lane, lane i lands at lds + 4 i.
+__device__ __forceinline__ void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (RG_LDS_AS void*)lds, 4, 0, 0);
+}
+
+// Copies n 4-byte words (unit 4) or 16-byte pieces (unit 16) from src to the
+// LDS array dst, 64 units per wave instruction; lanes past n copy nothing.
+template <int UNIT>
+__device__ __forceinline__ void tiny_copy(const void* src, void* dst, int n, int wave, int lane) {
+  for (int c = wave; c * 64 < n; c += tiny::kThreads / 64) {
+    const int u = c * 64 + lane;
+    const char* g = static_cast<const char*>(src) + (int64_t)u * UNIT;
+    char* l = static_cast<char*>(dst) + c * 64 * UNIT;
+    if (u < n) {
+      if constexpr (UNIT == 16)
+        dma16(reinterpret_cast<const int8_t*>(g), reinterpret_cast<int8_t*>(l));
+      else
+        dma4(g, l);
+    }
+  }
+}
+
+// Max over the wave's 64 lanes, in every lane, without LDS: partners l ^ 32
+// and l ^ 16 by the gfx950 lane swaps, then l ^ 15, l ^ 7, l ^ 2, l ^ 1 by
+// DPP (dpp_partner); those six offsets span all 64 lanes under XOR.
+__device__ __forceinline__ uint32_t wave_max_xlane(uint32_t v) {
+  {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = p[0] > p[1] ? p[0] : p[1];
+  }
+  {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = p[0] > p[1] ? p[0] : p[1];
+  }
+  uint32_t t = (uint32_t)dpp_partner<8>((int32_t)v);
+  v = t > v ? t : v;
+  t = (uint32_t)dpp_partner<4>((int32_t)v);
+  v = t > v ? t : v;
+  t = (uint32_t)dpp_partner<2>((int32_t)v);
+  v = t > v ? t : v;
+  t = (uint32_t)dpp_partner<1>((int32_t)v);
+  return t > v ? t : v;
+}
+
+__device__ __forceinline__ float tiny_epi(int32_t acc, float cs, float b, int act, float p) {
+  switch (act) {
+    case rgmath::ACT_RELU: return epi_value<rgmath::ACT_RELU>(acc, cs, b, p);
+    case rgmath::ACT_SIGMOID: return epi_value<rgmath::ACT_SIGMOID>(acc, cs, b, p);
+    case rgmath::ACT_TANH: return epi_value<rgmath::ACT_TANH>(acc, cs, b, p);
+    case rgmath::ACT_GELU: return epi_value<rgmath::ACT_GELU>(acc, cs, b, p);
+    case rgmath::ACT_LEAKY_RELU: return epi_value<rgmath::ACT_LEAKY_RELU>(acc, cs, b, p);
+    case rgmath::ACT_SILU: return epi_value<rgmath::ACT_SILU>(acc, cs, b, p);
+    default: return epi_value<rgmath::ACT_NONE>(acc, cs, b, p);
+  }
+}
+
+__global__ __launch_bounds__(tiny::kThreads) void mlp_tiny_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                  TinyChain ch, SlotClear clear) {
+  __shared__ __attribute__((aligned(16))) float act[2][tiny::kActWords];
+  __shared__ __attribute__((aligned(16))) float bias[tiny::kBiasWords];
+  __shared__ __attribute__((aligned(16))) int8_t wl[kTinyWeightBytes];
+  __shared__ __attribute__((aligned(16))) int8_t qa[kTinyRows * tiny::kQaLd];
+  __shared__ uint32_t red[tiny::kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rows = ch.rows;
+  // the input lands as it is laid out in memory (row stride in_f)
+  tiny_copy<4>(x, act[0], rows * ch.l[0].in_f, wave, lane);
+  for (int l = 0, woff = 0; l < ch.n; l++) {
+    tiny_copy<16>(ch.l[l].w, wl + woff, ch.l[l].out_f * ch.l[l].kpad / 16, wave, lane);
+    tiny_copy<4>(ch.l[l].bias, bias + l * kTinyWidth, ch.l[l].out_f, wave, lane);
+    woff += ch.l[l].out_f * ch.l[l].kpad;
+  }
+  // the other slot set (clear_slots without its block-size read, whose wait
+  // would also wait for the copies above)
+  for (int64_t i = tid; i < clear.n; i += tiny::kThreads) clear.p[i] = 0u;
+  wait_vmcnt<0>();
+  __syncthreads();
+  int cur = 0, ld = ch.l[0].in_f;  // the current activation buffer and its row stride
+  for (int l = 0, woff = 0; l < ch.n; l++) {
+    const TinyLayer L = ch.l[l];
+    const float* src = act[cur];
+    // The input's absmax: the first layer folds its input; a later layer's
+    // per-wave partials were left in red by the previous layer's epilogue.
+    if (l == 0) {
+      uint32_t m0 = 0;
+      for (int e = tid; e < rows * L.in_f; e += tiny::kThreads) {
+        const int r = e / L.in_f, k = e - r * L.in_f;
+        const uint32_t key = rgmath::absmax_key(src[r * ld + k]);
+        m0 = key > m0 ? key : m0;
+      }
+      m0 = wave_max_xlane(m0);
+      if (lane == 0) red[wave] = m0;
+      __syncthreads();
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int w = 0; w < tiny::kThreads / 64; w++) m = red[w] > m ? red[w] : m;
+    const float scale = rgmath::scale_from_absmax(rgmath::bitsf(m));
+    const float inv = 1.0f / scale;
+    if (tid == 0 && L.slot) L.slot[0] = m;
+    const int kp4 = L.kpad / 4;
+    for (int e = tid; e < rows * kp4; e += tiny::kThreads) {
+      const int r = e / kp4, w = e - r * kp4, k = 4 * w;
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) v[c] = k + c < L.in_f ? src[r * ld + k + c] : 0.0f;
+      reinterpret_cast<uint32_t*>(qa + r * tiny::kQaLd)[w] = pack4(v[0], v[1], v[2], v[3], inv);
+    }
+    __syncthreads();
+    const float cs = scale * L.w_scale;
+    const bool last = l + 1 == ch.n;
+    float* const dst = act[cur ^ 1];
+    // output-major: a wave's lanes share a weight row (broadcast reads) and
+    // take consecutive operand rows
+    uint32_t mo = 0;  // absmax of the outputs this thread writes (the next layer's input)
+    for (int e = tid; e < rows * L.out_f; e += tiny::kThreads) {
+      const int n = e / rows, r = e - n * rows;
+      const v4i* qr = reinterpret_cast<const v4i*>(qa + r * tiny::kQaLd);
+      const v4i* wr = reinterpret_cast<const v4i*>(wl + woff + n * kTinyWidth);
+      // Kpad == kTinyWidth: every fragment read is issued before the sums
+      v4i a[kTinyWidth / 16], b[kTinyWidth / 16];
+#pragma unroll
+      for (int k = 0; k < kTinyWidth / 16; k++) {
+        a[k] = qr[k];
+        b[k] = wr[k];
+      }
+      int32_t acc = 0;
+#pragma unroll
+      for (int k = 0; k < kTinyWidth / 16; k++) {
+        acc = __builtin_amdgcn_sdot4(a[k][0], b[k][0], acc, false);
+        acc = __builtin_amdgcn_sdot4(a[k][1], b[k][1], acc, false);
+        acc = __builtin_amdgcn_sdot4(a[k][2], b[k][2], acc, false);
+        acc = __builtin_amdgcn_sdot4(a[k][3], b[k][3], acc, false);
+      }
+      const float v = tiny_epi(acc, cs, bias[l * kTinyWidth + n], L.act, L.act_param);
+      if (last) {
+        y[r * L.out_f + n] = v;
+      } else {
+        dst[r * tiny::kActLd + n] = v;
+        const uint32_t key = rgmath::absmax_key(v);
+        mo = key > mo ? key : mo;
+      }
+    }
+    // every thread read red before the barrier after the quantization
+    if (!last) {
+      mo = wave_max_xlane(mo);
+      if (lane == 0) red[wave] = mo;
+    }
+    woff += L.out_f * L.kpad;
+    cur ^= 1;
+    ld = tiny::kActLd;
+    __syncthreads();
+  }
+}
+
+void launch_mlp_tiny(const float* x, float* y, const TinyChain& ch, SlotClear clear, hipStream_t s) {
+  int wbytes = 0;
+  bool ok = ch.n >= 1 && ch.n <= kTinyMaxLayers && ch.rows >= 1 && ch.rows <= kTinyRows;
+  for (int l = 0; ok && l < ch.n; l++) {
+    const TinyLayer& L = ch.l[l];
+    ok = L.in_f >= 1 && L.in_f <= kTinyWidth && L.out_f >= 1 && L.out_f <= kTinyWidth && L.kpad == kTinyWidth &&
+         (l == 0 || L.in_f == ch.l[l - 1].out_f) && L.w && L.bias && (reinterpret_cast<uintptr_t>(L.w) & 15) == 0;
+    wbytes += L.out_f * L.kpad;
+  }
+  if (!ok || wbytes > kTinyWeightBytes || (reinterpret_cast<uintptr_t>(x) & 3) || (reinterpret_cast<uintptr_t>(y) & 3))
+    throw std::logic_error("mlp_tiny: the chain does not fit the one-workgroup kernel");
+  RG_LAUNCH(mlp_tiny_kernel, dim3(1), dim3(tiny::kThreads), 0, s, x, y, ch, clear);
+}
+
 void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
                             const Epilogue& ep, hipStream_t s) {
   launch_gemm_narrow_t<kModeF16>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(B), M, N,

@@ -162,7 +162,10 @@ struct OpPlan {
 struct Plan {
   std::vector<int64_t> in_shape, out_shape;
   bool capture = false;  // made for capture runs (no conv-pool fusion)
-  bool persistent = true;  // may launch persistent grids (fused requantization, one-pass input quantization)
+  // made while persistent grids (fused requantization, one-pass input
+  // quantization) were allowed
+  bool persistent = true;
+  bool tiny = false;       // the whole program is one mlp_tiny_kernel launch (by the first op)
   int64_t in_len = 0, out_len = 0;
   std::vector<OpPlan> ops;
   size_t f32_elems = 0, q_bytes = 0, ylo_elems = 0;
@@ -861,6 +864,24 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     size_t qb = op.kind == OP_LINEAR ? (size_t)(pl.Mpad * op.Kpad) : (size_t)pl.in_len;
     plan->q_bytes = std::max(plan->q_bytes, qb);
   }
+  // A program of small INT8 Linears on the same rows runs as one kernel in
+  // one workgroup (launch_mlp_tiny, the same arithmetic op by op): the first
+  // op launches it and the others launch nothing.  Not in capture plans,
+  // which store every op's operand and output; RGNPU_TINY_MLP=0 turns it off.
+  {
+    const char* te = getenv("RGNPU_TINY_MLP");
+    bool tiny = P->precision == RGNPU_PRECISION_INT8 && !plan->capture && !(te && atoi(te) == 0) && nops >= 1 &&
+                nops <= (size_t)kTinyMaxLayers;
+    int64_t wbytes = 0;
+    for (size_t i = 0; tiny && i < nops; i++) {
+      const Op& op = *P->ops[i];
+      const OpPlan& pl = plan->ops[i];
+      tiny = op.kind == OP_LINEAR && pl.rows >= 1 && pl.rows <= kTinyRows && pl.rows == plan->ops[0].rows &&
+             op.in_f <= kTinyWidth && op.out_f <= kTinyWidth && op.Kpad == kTinyWidth;
+      wbytes += op.out_f * op.Kpad;
+    }
+    plan->tiny = tiny && wbytes <= kTinyWeightBytes;
+  }
   // Requantization fused into the producing GEMM: an INT8 Linear on the
   // unsplit MFMA GEMM whose next computing op is a Linear reading the same
   // rows (its absmax is this op's emitted slot).  Its barrier words join the
@@ -875,8 +896,8 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
   // two host runs of a program have overlapped, its worker runs therefore use
   // plans with the separate quantize kernels (the same arithmetic); those
   // runs are bound by their host copies anyway.
-  const bool persistent_ok = P->use_persistent;
-  plan->persistent = persistent_ok;
+  const bool persistent_ok = P->use_persistent && !plan->tiny;
+  plan->persistent = P->use_persistent;
   bool any_requant = false;
   for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8 && persistent_ok; i++) {
     const Op& op = *P->ops[i];
@@ -1201,6 +1222,30 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
     uint32_t* emit = pl.emit_slot >= 0 ? slots + pl.emit_slot : nullptr;
     switch (op.kind) {
       case OP_LINEAR: {
+        if (plan.tiny) {
+          pre = launch_events_used();
+          if (i == 0) {
+            TinyChain ch;
+            ch.n = (int32_t)P->ops.size();
+            ch.rows = (int32_t)pl.rows;
+            for (size_t l = 0; l < P->ops.size(); l++) {
+              const Op& o = *P->ops[l];
+              TinyLayer& t = ch.l[l];
+              t.w = o.d_w.as<int8_t>();
+              t.bias = o.d_bias.as<float>();
+              t.slot = slots + plan.ops[l].slot_base;
+              t.in_f = (int32_t)o.in_f;
+              t.out_f = (int32_t)o.out_f;
+              t.kpad = (int32_t)o.Kpad;
+              t.act = o.act;
+              t.act_param = o.act_param;
+              t.w_scale = o.w_scale;
+            }
+            launch_mlp_tiny(in, y, ch, clear, s);
+            first_launched();
+          }
+          break;
+        }
         if (f32) {  // mod.rs:263-273: matmul, then the bias
           pre = launch_events_used();
           if (pl.rows > 0) {
@@ -1478,8 +1523,10 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
       // operand instead (INT8 requantization, FP16 hand-off), or the conv
       // pools in its epilogue (its buffer then holds the pool's output, which
       // is the output of the MaxPool2d op; an FP32 conv's absorbed Act op
-      // likewise has none of its own).
-      const bool has_out = !pl.requant && !pl.handoff && !pl.pool_r16 && !(pl.pool_fused && op.kind != OP_POOL);
+      // likewise has none of its own), or the program runs as one tiny
+      // kernel (only the last op's output leaves its LDS).
+      const bool has_out = !pl.requant && !pl.handoff && !pl.pool_r16 && !(pl.pool_fused && op.kind != OP_POOL) &&
+                           !(plan.tiny && pl.out_buf != BUF_OUTPUT);
       plan.tap_out_ok[i] = has_out;
       if (has_out && pl.out_len > 0)
         RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),

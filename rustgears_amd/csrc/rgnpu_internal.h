@@ -196,6 +196,29 @@ void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, 
 bool gemm_narrow_xq_supported(int64_t K, int64_t Kpad);
 void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t K, int64_t Kpad,
                            const Epilogue& ep, int8_t* q_out, float* scale_out, hipStream_t s);
+// A whole program of small INT8 Linears (npu.rs:307-318 per op: the input
+// quantized per tensor with its own absmax, quantize.rs:18-24, then the
+// fused GEMM, quantize.rs:93-118) in one workgroup, for programs whose every
+// op is a Linear on the same rows: at most kTinyMaxLayers layers, kTinyRows
+// rows, kTinyWidth input and output features, Kpad == kTinyWidth (the INT8
+// Kpad of any K <= kTinyWidth), and kTinyWeightBytes of weights (out_f x Kpad
+// per layer) in all.  Layer l reads
+// w [out_f, Kpad] (i8, zero K padding) and writes its input's absmax key into
+// slot[0] (a spread slot the run zeroed); the last layer writes y [rows, out_f].
+constexpr int kTinyMaxLayers = 8, kTinyRows = 64, kTinyWidth = 128, kTinyWeightBytes = 48 * 1024;
+static_assert(kTinyWidth == kKPad, "one Kpad for every layer of a tiny program");
+struct TinyLayer {
+  const int8_t* w = nullptr;
+  const float* bias = nullptr;
+  uint32_t* slot = nullptr;
+  int32_t in_f = 0, out_f = 0, kpad = 0, act = 0;
+  float act_param = 0.0f, w_scale = 1.0f;
+};
+struct TinyChain {
+  TinyLayer l[kTinyMaxLayers];
+  int32_t n = 0, rows = 0;
+};
+void launch_mlp_tiny(const float* x, float* y, const TinyChain& ch, SlotClear clear, hipStream_t s);
 void launch_gemm_narrow_f16(const uint16_t* A, const uint16_t* B, int64_t M, int64_t N, int64_t Kpad_h,
                             const Epilogue& ep, hipStream_t s);
 void launch_gemm_narrow_f32(const float* A, const float* B, int64_t M, int64_t N, int64_t Kpad_f, const Epilogue& ep,
