@@ -17,7 +17,10 @@ Bit for bit against the oracle, capture taps included:
 * the one-row form that quantizes its own f32 input: with the input's own
   absmax (the run's first Linear) and with the producer's, K at the largest
   row it stages (8192) and just past it, K % 4 != 0 and an unaligned input
-  (both take the separate quantize pass).
+  (both take the separate quantize pass);
+* one-row GEMVs after a one-row GEMV whose rows are past that staging (the
+  producer's absmax, a separate quantize pass), without capture: a ragged K,
+  the G layer-2 shape, K % 4 != 0, and NaN and +-inf in the input.
 """
 import numpy as np
 import pytest
@@ -170,3 +173,44 @@ def test_gemv_one_row_unaligned_input(rg, ref):
     sess.synchronize()
     assert_bitexact_f32(d_y.download((1, 300)), want, "gemv one row, aligned input")
     sess.close()
+
+
+LONG_ROW_CASES = [
+    # (dims, what): the second layer's row is longer than gemv_xq stages
+    ([1000, 9004, 100], "ragged K past the staged row"),
+    ([3000, 28672, 4096], "G layer-2 shape"),
+    ([1000, 8198, 64], "K % 4 != 0"),
+]
+
+
+@pytest.mark.parametrize("dims,what", LONG_ROW_CASES, ids=[c[1] for c in LONG_ROW_CASES])
+def test_gemv_one_row_after_a_long_row(rg, ref, dims, what):
+    layers = _mlp(rg, dims, seed=dims[1] + 3, act="gelu")
+    x = rg.randn([1, dims[0]])
+    want = ref.RefProgram(layers).run(x)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    y = sess.run(x)
+    y2 = sess.run(x)
+    recs = sess.last_npu_profile().records
+    sess.close()
+    assert_bitexact_f32(y, want, f"gemv long row {what}")
+    assert_bitexact_f32(y2, want, f"gemv long row {what} (second run)")
+    assert recs[1].kernel_ns > 0, recs[1]
+    check_against_oracle(rg, ref, layers, x, f"gemv long row {what} (capture)")
+
+
+def test_gemv_long_row_special_values(rg, ref):
+    """NaN and +-inf in the long row the second GEMV reads (planted through
+    the first layer's bias): the absmax is +inf, so the scale is +inf and
+    every value quantizes to 0 (NaN * 0 and inf * 0 are NaN, which quantize
+    to 0 as well); then a NaN-only column with finite others."""
+    for what, plant in (("inf and NaN", {5: np.nan, 9: np.inf, 12: -np.inf}), ("NaN only", {5: np.nan})):
+        layers = _mlp(rg, [512, 9000, 64], seed=3, act="gelu")  # GELU keeps NaN and +inf (-inf becomes NaN)
+        for col, v in plant.items():
+            layers[0].bias[col] = v
+        x = rg.randn([1, 512])
+        want = ref.RefProgram(layers).run(x)
+        sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+        y = sess.run(x)
+        sess.close()
+        assert_bitexact_f32(y, want, f"gemv long row {what}")
