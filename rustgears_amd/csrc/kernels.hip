@@ -2284,14 +2284,17 @@ __device__ __forceinline__ int udiv(int n, uint32_t mag) { return mag ? (int)__u
 // The block's absmax for the next op: the 4 waves' maxima meet in LDS and
 // one atomic per block raises the image's slot (per image) or one partial of
 // the spread slot (per tensor), so an image slot takes one atomic per block
-// rather than one per wave.  Every thread of the block calls it.
+// rather than one per wave.  Every thread of the block (NW waves) calls it.
+template <int NW = 4>
 __device__ __forceinline__ void conv_block_absmax(const Epilogue& ep, int b, uint32_t amax, uint32_t* red, int lane) {
   if (!ep.absmax_out) return;
   amax = wave_max_u32(amax);
   if (lane == 0) red[threadIdx.x >> 6] = amax;
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t m = max(max(red[0], red[1]), max(red[2], red[3]));
+    uint32_t m = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = red[w] > m ? red[w] : m;
     if (m) {
       if (ep.absmax_out_per_image) {
         atomicMax(ep.absmax_out + b, m);
@@ -2343,13 +2346,15 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
 // next row in fragment j + R16 of the same lane and pixel p + 1 in lane ^ 1.
 // An even lane takes its window in the reference's order (0,0), (0,1),
 // (1,0), (1,1) with pool_take from -inf (maxpool2_kernel's rule), and the
-// absmax for the next op is over the pooled values.
+// absmax for the next op is over the pooled values.  LDS: the pooled values
+// go to the image's planes lout [O, OH/2, OW/2] in LDS instead, and the
+// block's absmax is left to the caller (the lane's key is returned).
 
-template <int TM, int TN, int ACT, int R16>
-__device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
-                                                         const Epilogue& ep, int b, int o0,
-                                                         const int (&pix)[TN / 64], float csc, int lane,
-                                                         uint32_t* red) {
+template <int TM, int TN, int ACT, int R16, bool LDS = false, int NW = 4>
+__device__ __forceinline__ uint32_t conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
+                                                             const Epilogue& ep, int b, int o0,
+                                                             const int (&pix)[TN / 64], float csc, int lane,
+                                                             uint32_t* red, float* lout = nullptr) {
   constexpr int FM = TM / 16, FN = TN / 64;
   static_assert(FN % (2 * R16) == 0, "a wave's pixels are whole pairs of output rows");
   const int O = (int)cs.O;
@@ -2359,7 +2364,7 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
   // the pooled pixel of each even-row fragment (once per lane), stored
   // through a bounded resource over the image's pooled planes with 32-bit
   // offsets o * PL + pp (host-checked: O * PL * 4 < 2^31)
-  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(ep.y + (int64_t)b * O * PL);
+  const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(LDS ? nullptr : ep.y + (int64_t)b * O * PL);
   float4 b4[FM];  // the lane's 4 output channels of each row block (bias padded to Opad)
 #pragma unroll
   for (int i = 0; i < FM; i++) b4[i] = *reinterpret_cast<const float4*>(ep.bias + o0 + i * 16 + (lane >> 4) * 4);
@@ -2399,13 +2404,83 @@ __device__ __forceinline__ void conv_band_epilogue_pool2(const v4i (&acc)[TM / 1
           best = pool_take(best, h[jn]);
         }
         const bool ok = pp[j] >= 0 && o < O;
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), ry,
-                                              (int)(ok ? (uint32_t)(o * PL + pp[j]) * 4u : kDropOffset), 0, 0);
+        if constexpr (LDS) {
+          if (ok) lout[o * PL + pp[j]] = best;
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), ry,
+                                                (int)(ok ? (uint32_t)(o * PL + pp[j]) * 4u : kDropOffset), 0, 0);
+        }
         const uint32_t key = ok ? (ACT == rgmath::ACT_RELU ? rgmath::fbits(best) : rgmath::absmax_key(best)) : 0u;
         amax = key > amax ? key : amax;
       }
     }
-  conv_block_absmax(ep, b, amax, red, lane);
+  if constexpr (!LDS) conv_block_absmax<NW>(ep, b, amax, red, lane);
+  return amax;
+}
+
+// The band conv's MFMA part: wave `wave`'s TN / 4 pixels of the block from
+// output pixel p0 (pix[j]: fragment j's pixel in this lane), summed over the
+// LDS band (output row oy0's band row first, channel-last with cp channels
+// per pixel, Wp pixels per row) against TM weight rows of wstride bytes.
+// Each MFMA B fragment is one ds_read_b128 (cp >= 16) or four ds_read_b32
+// (CP4) of the band; taps past k * k and pixels past L read zero16.
+struct BandGeom {
+  int OW, L, oy0, st, Wp, cp, k, kk, KP, wstride;
+};
+
+template <int TM, int TN, bool CP4>
+__device__ __forceinline__ void conv_band_mma(const int8_t* wts, const int8_t* band, const int8_t* zero16,
+                                              const BandGeom& g, int p0, int wave, int lane, int (&pix)[TN / 64],
+                                              v4i (&acc)[TM / 16][TN / 64]) {
+  constexpr int WTN = TN / 4, FM = TM / 16, FN = WTN / 16;
+  const int OW = g.OW, L = g.L, oy0 = g.oy0, st = g.st, Wp = g.Wp, cp = g.cp, k = g.k, kk = g.kk, KP = g.KP,
+            wstride = g.wstride;
+  // the byte offset of each pixel's tap (0, 0), channel 0
+  const uint32_t owmag_k = div_magic((uint32_t)OW), kmag = div_magic((uint32_t)k), cpmag = div_magic((uint32_t)cp);
+  int rowoff[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    pix[j] = p0 + wave * WTN + j * 16 + (lane & 15);
+    const int oy = udiv(pix[j], owmag_k), ox = pix[j] - oy * OW;
+    rowoff[j] = pix[j] < L ? ((oy - oy0) * st * Wp + ox * st) * cp : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+  for (int k0 = 0; k0 < KP; k0 += 64) {
+    const int kb = k0 + (lane >> 4) * 16;  // this lane's 16-byte K chunk
+    v4i af[FM], bf[FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(wts + (i * 16 + (lane & 15)) * wstride + kb);
+    if (!CP4) {
+      const int tap = udiv(kb, cpmag), c0 = kb - tap * cp;
+      const int ki = udiv(tap, kmag), kj = tap - ki * k;
+      const int toff = (ki * Wp + kj) * cp + c0;
+#pragma unroll
+      for (int j = 0; j < FN; j++) {
+        const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
+        bf[j] = *reinterpret_cast<const v4i*>(a);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int tap = (kb >> 2) + e;
+        const int ki = udiv(tap, kmag), kj = tap - ki * k;
+        const int toff = (ki * Wp + kj) * 4;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
+          bf[j][e] = *reinterpret_cast<const int*>(a);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
 }
 
 constexpr int64_t kConvSelfAbsmaxMax = 16384;
@@ -2647,53 +2722,11 @@ __global__ __launch_bounds__(256, CP4 ? 4 : 1) void conv_band_kernel(const int8_
   }
   __syncthreads();
 
-  // 3. per-lane pixels and the byte offset of their tap (0, 0), channel 0.
-  const uint32_t owmag_k = div_magic((uint32_t)OW), kmag = div_magic((uint32_t)k), cpmag = div_magic((uint32_t)cp);
-  int pix[FN], rowoff[FN];
-#pragma unroll
-  for (int j = 0; j < FN; j++) {
-    pix[j] = p0 + wave * WTN + j * 16 + (lane & 15);
-    const int oy = udiv(pix[j], owmag_k), ox = pix[j] - oy * OW;
-    rowoff[j] = pix[j] < L ? ((oy - oy0) * st * Wp + ox * st) * cp : -1;
-  }
+  // 3. per-lane pixels and their sums over the band
+  const BandGeom geo{OW, L, oy0, st, Wp, cp, k, kk, KP, wstride};
+  int pix[FN];
   v4i acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; i++)
-#pragma unroll
-    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-  for (int k0 = 0; k0 < KP; k0 += 64) {
-    const int kb = k0 + (lane >> 4) * 16;  // this lane's 16-byte K chunk
-    v4i af[FM], bf[FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(wts + (i * 16 + (lane & 15)) * wstride + kb);
-    if (!CP4) {
-      const int tap = udiv(kb, cpmag), c0 = kb - tap * cp;
-      const int ki = udiv(tap, kmag), kj = tap - ki * k;
-      const int toff = (ki * Wp + kj) * cp + c0;
-#pragma unroll
-      for (int j = 0; j < FN; j++) {
-        const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
-        bf[j] = *reinterpret_cast<const v4i*>(a);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int tap = (kb >> 2) + e;
-        const int ki = udiv(tap, kmag), kj = tap - ki * k;
-        const int toff = (ki * Wp + kj) * 4;
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-          const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
-          bf[j][e] = *reinterpret_cast<const int*>(a);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-      for (int j = 0; j < FN; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-  }
+  conv_band_mma<TM, TN, CP4>(wts, band, zero16, geo, p0, wave, lane, pix, acc);
   float csc;
   if constexpr (XF)
     csc = img_scale * ep.w_scale;
@@ -2903,6 +2936,251 @@ bool launch_conv_f32in(const float* x, const int8_t* Wq, const ConvShape& cs, co
                : try_conv_band_tn<64, false, true>(xb, Wq, cs, ep, s, sa, clear);
   return cp4 ? try_conv_band_tn<32, true, true>(xb, Wq, cs, ep, s, sa, clear)
              : try_conv_band_tn<32, false, true>(xb, Wq, cs, ep, s, sa, clear);
+}
+
+// ---------------------------------------------------------------------------
+// Two INT8 conv + 2 x 2 max pool stages on one image per workgroup
+// (npu.rs:319-390, op after op): conv A (C <= 4 channels, 3 x 3, stride 1,
+// pad 1, on a 32 x 32 image) with ReLU or no activation, its pool, then
+// conv B (OA -> OB channels, the same window) and its pool.  A conv's
+// activation scale is per image (npu.rs:341-351), and conv B's is the absmax
+// of this image's pooled conv A output, which the workgroup holds in LDS:
+// nothing crosses workgroups, the pooled intermediate never leaves LDS, and
+// one launch replaces two.  Every step is the arithmetic of conv_band_kernel
+// (the band quantized with the image's own scale, conv_band_mma, the pooled
+// epilogue's window rule), so the outputs are the same bit for bit.
+// The workgroup is 16 waves in four groups of 4 (four waves per SIMD).
+//  0. Each thread loads one unit of the image (4 channels x 4 pixels of one
+//     row: 256 units cover 32 x 32; threads 256.. load them again),
+//     and a share of both convs' weights.
+//  1. The image's absmax from those registers (every pixel is in a window);
+//     its key goes to conv A's slot, as the separate conv would publish it.
+//  2. The unit, quantized, fills conv A's channel-last band (all 34 rows).
+//  3. Conv A in four 256-pixel blocks, one per wave group, each pooled into
+//     the LDS planes.
+//  4. The planes' absmax (conv B's per-image scale; its key goes to conv B's
+//     slot, as pool A's epilogue would have raised it).
+//  5. The planes, quantized, fill conv B's band.
+//  6. Conv B over all 256 pixels, each wave group taking a quarter of the
+//     output channels, pooled into y with the block's absmax raised for the
+//     next op (conv_block_absmax).
+// ---------------------------------------------------------------------------
+constexpr int kPairSide = 32;  // conv A's image side; conv B's is half of it
+
+struct PairLds {
+  int wa, wb, band_a, zero_a, band_b, zero_b, plane, total;
+};
+
+// LDS byte offsets (each 16-byte aligned): the weights (rows of Kpad + 16
+// bytes, as conv_band_kernel stages them), the bands with a zero block each,
+// and the pooled planes [OA, 16, 16] f32.
+static __host__ __device__ inline PairLds pair_lds(int OA, int OB, int KPA, int KPB) {
+  const int sa = kPairSide + 2, sb = kPairSide / 2 + 2;
+  PairLds l{};
+  l.wa = 0;
+  l.wb = (OA * (KPA + 16) + 15) & ~15;
+  l.band_a = l.wb + ((OB * (KPB + 16) + 15) & ~15);
+  l.zero_a = l.band_a + ((sa * sa * 4 + 15) & ~15);
+  l.band_b = l.zero_a + 16;
+  l.zero_b = l.band_b + ((sb * sb * OA + 15) & ~15);
+  l.plane = l.zero_b + 16;
+  l.total = l.plane + OA * (kPairSide / 2) * (kPairSide / 2) * 4;
+  return l;
+}
+
+constexpr int kPairThreads = 1024;  // 16 waves: four groups of 4, four waves per SIMD
+constexpr int kPairWbUnits = 2;     // 16-byte weight units of conv B per thread at most (OB * KPB <= 2 * 1024 * 16)
+
+template <int OA, int OB, int ACTA, int ACTB>
+__global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const float* __restrict__ x,
+                                                                      const int8_t* __restrict__ WA,
+                                                                      const int8_t* __restrict__ WB, ConvShape csA,
+                                                                      ConvShape csB, Epilogue epA, Epilogue epB,
+                                                                      SlotClear clear) {
+  constexpr int S = kPairSide, PS = S / 2, SA = S + 2, SB = PS + 2, PL = PS * PS, NT = kPairThreads, NW = NT / 64;
+  constexpr int NG = NW / 4;  // wave groups
+  static_assert(OA % 16 == 0 && OB % (16 * NG) == 0, "channel blocks of 16; conv B's channels split over the groups");
+  extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
+  __shared__ uint32_t red[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2, wl = wave & 3, b = blockIdx.x;
+  const int C = (int)csA.C, KPA = (int)csA.Kpad, KPB = (int)csB.Kpad;
+  // the shapes with their sides as constants, so the epilogues' divisions fold
+  ConvShape sa = csA, sb = csB;
+  sa.O = OA;
+  sa.OH = sa.OW = S;
+  sb.O = OB;
+  sb.OH = sb.OW = PS;
+  const PairLds ly = pair_lds(OA, OB, KPA, KPB);
+  int8_t* const wa = dsm + ly.wa;
+  int8_t* const wb = dsm + ly.wb;
+  int8_t* const band_a = dsm + ly.band_a;
+  int8_t* const band_b = dsm + ly.band_b;
+  float* const plane = reinterpret_cast<float*>(dsm + ly.plane);
+
+  // 0. unit tid % 256 of the image (channels 0-3 of pixels x4 .. x4 + 3 of
+  // row y; channels past C read zeros through the bounded resource), which
+  // threads 256.. load again and do not store, and the weights.  Weight rows
+  // are contiguous in memory (KPA, KPB bytes): unit i of a conv's weights is
+  // bytes [16 i, 16 i + 16).  Every load is issued (a unit past the end is
+  // clamped and not stored), so no branch leaves a register pending.
+  const int unit = tid & 255, y = unit >> 3, x4 = (unit & 7) * 4;
+  const float* img = x + (int64_t)b * C * S * S;
+  const __amdgpu_buffer_rsrc_t rimg =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(img), 0, (int)((uint32_t)(C * S * S) * 4u), 0x00020000);
+  v4f u[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++)
+    u[q] = __builtin_bit_cast(
+        v4f, __builtin_amdgcn_raw_buffer_load_b128(rimg, (int)((uint32_t)((q * S + y) * S + x4) * 4u), 0, 0));
+  const int kca = KPA / 16, kcb = KPB / 16, na = OA * kca, nb = OB * kcb;
+  const uint32_t kcamag = div_magic((uint32_t)kca), kcbmag = div_magic((uint32_t)kcb);
+  const v4i wav = reinterpret_cast<const v4i*>(WA)[tid < na ? tid : na - 1];
+  v4i wbv[kPairWbUnits];
+#pragma unroll
+  for (int t = 0; t < kPairWbUnits; t++) {
+    const int i = tid + NT * t;
+    wbv[t] = reinterpret_cast<const v4i*>(WB)[i < nb ? i : nb - 1];
+  }
+  // both bands and their zero blocks to zero (they are contiguous)
+  for (int i = tid; i < (ly.plane - ly.band_a) / 16; i += NT) reinterpret_cast<v4i*>(band_a)[i] = v4i{0, 0, 0, 0};
+  clear_slots(clear);
+  if (tid < na) {
+    const int row = udiv(tid, kcamag), c16 = tid - row * kca;
+    *reinterpret_cast<v4i*>(wa + row * (KPA + 16) + c16 * 16) = wav;
+  }
+#pragma unroll
+  for (int t = 0; t < kPairWbUnits; t++) {
+    const int i = tid + NT * t;
+    if (i < nb) {
+      const int row = udiv(i, kcbmag), c16 = i - row * kcb;
+      *reinterpret_cast<v4i*>(wb + row * (KPB + 16) + c16 * 16) = wbv[t];
+    }
+  }
+  // 1. the image's absmax (NaN ignored, like f32::max)
+  float m = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(u[q][0])), __builtin_fabsf(u[q][1]));
+    m = __builtin_fmaxf(__builtin_fmaxf(m, __builtin_fabsf(u[q][2])), __builtin_fabsf(u[q][3]));
+  }
+  uint32_t w = wave_max_u32(rgmath::fbits(m));
+  if (lane == 0) red[wave] = w;
+  __syncthreads();
+  uint32_t ta = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; i++) ta = red[i] > ta ? red[i] : ta;
+  if (tid == 0) ep_absmax_publish(epA.absmax_in, b, ta);
+  const float scale_a = rgmath::scale_from_absmax(rgmath::bitsf(ta));
+  // 2. conv A's band: pixel (y, x) at word (y + 1) * SA + x + 1, channels 0-3
+  if (tid < 256) {
+    const float inv = 1.0f / scale_a;
+    uint32_t* const bw = reinterpret_cast<uint32_t*>(band_a) + (y + 1) * SA + x4 + 1;
+#pragma unroll
+    for (int xx = 0; xx < 4; xx++) {
+      const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(u[0][xx] * inv);
+      const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(u[1][xx] * inv);
+      const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(u[2][xx] * inv);
+      const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(u[3][xx] * inv);
+      const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u), hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+      bw[xx] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+  }
+  __syncthreads();
+  // 3. conv A, pooled into the planes: the wave groups take the 256-pixel
+  // blocks in turn
+  const float csc_a = scale_a * epA.w_scale;
+  const BandGeom ga{S, S * S, 0, 1, SA, 4, 3, 9, KPA, KPA + 16};
+  uint32_t ma = 0;
+#pragma unroll 1
+  for (int blk = grp; blk < (S * S) / 256; blk += NG) {
+    int pix[4];
+    v4i acc[OA / 16][4];
+    conv_band_mma<OA, 256, true>(wa, band_a, dsm + ly.zero_a, ga, blk * 256, wl, lane, pix, acc);
+    const uint32_t t = conv_band_epilogue_pool2<OA, 256, ACTA, 2, true>(acc, sa, epA, b, 0, pix, csc_a, lane, red,
+                                                                        plane);
+    ma = t > ma ? t : ma;
+  }
+  // 4. conv B's scale: the absmax of the pooled planes
+  w = wave_max_u32(ma);
+  __syncthreads();  // every plane value is written, and red is free again
+  if (lane == 0) red[wave] = w;
+  __syncthreads();
+  uint32_t tb = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; i++) tb = red[i] > tb ? red[i] : tb;
+  if (tid == 0) ep_absmax_publish(epB.absmax_in, b, tb);
+  const float scale_b = rgmath::scale_from_absmax(rgmath::bitsf(tb));
+  // 5. conv B's band: pixel p of the planes, channel group g at word
+  // ((p / 16 + 1) * SB + p % 16 + 1) * (OA / 4) + g
+  {
+    const float inv = 1.0f / scale_b;
+    uint32_t* const bw = reinterpret_cast<uint32_t*>(band_b);
+#pragma unroll
+    for (int t = 0; t < (OA / 4) * PL / NT; t++) {
+      const int e = tid + NT * t, p = e & (PL - 1), g = e / PL;
+      const float* src = plane + (4 * g) * PL + p;
+      const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(src[0] * inv);
+      const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(src[PL] * inv);
+      const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(src[2 * PL] * inv);
+      const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(src[3 * PL] * inv);
+      const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u), hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+      bw[((p / PS + 1) * SB + (p % PS) + 1) * (OA / 4) + g] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+  }
+  __syncthreads();
+  // 6. conv B, pooled into y: each wave group takes OB / NG output channels
+  constexpr int OH = OB / NG;
+  const BandGeom gb{PS, PL, 0, 1, SB, OA, 3, 9, KPB, KPB + 16};
+  int pix[4];
+  v4i acc[OH / 16][4];
+  conv_band_mma<OH, 256, false>(wb + grp * OH * (KPB + 16), band_b, dsm + ly.zero_b, gb, 0, wl, lane, pix, acc);
+  conv_band_epilogue_pool2<OH, 256, ACTB, 1, false, NW>(acc, sb, epB, b, grp * OH, pix, scale_b * epB.w_scale, lane,
+                                                        red);
+}
+
+bool conv_pool_pair_supported(const ConvShape& a, const ConvShape& b) {
+  constexpr int S = kPairSide;
+  const bool ok_a = a.C >= 1 && a.C <= 4 && a.cp == 4 && a.H == S && a.W == S && a.k == 3 && a.stride == 1 &&
+                    a.pad == 1 && a.OH == S && a.OW == S && a.O == 32 && a.Opad == 32 && a.Kpad == conv_kpad(a.C, 3);
+  const bool ok_b = b.C == 32 && b.cp == 32 && b.H == S / 2 && b.W == S / 2 && b.k == 3 && b.stride == 1 &&
+                    b.pad == 1 && b.OH == S / 2 && b.OW == S / 2 && b.O == 64 && b.Opad == 64 &&
+                    b.Kpad == conv_kpad(32, 3) && b.n == a.n;
+  return ok_a && ok_b && a.n >= 1 && a.n <= 65535 && 64 * (b.Kpad / 16) <= kPairThreads * kPairWbUnits &&
+         pair_lds(32, 64, (int)a.Kpad, (int)b.Kpad).total <= 160 * 1024 - 64;
+}
+
+template <int ACTA, int ACTB>
+static void launch_pair_t(const float* x, const int8_t* WA, const int8_t* WB, const ConvShape& a, const ConvShape& b,
+                          const Epilogue& ea, const Epilogue& eb, SlotClear clear, hipStream_t s) {
+  const int lds = pair_lds(32, 64, (int)a.Kpad, (int)b.Kpad).total;
+  const void* fn = reinterpret_cast<const void*>(&conv_pool_pair_kernel<32, 64, ACTA, ACTB>);
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 64) != hipSuccess)
+      throw std::runtime_error("conv pair: the dynamic LDS limit could not be raised");
+    attr_set = true;
+  }
+  RG_LAUNCH((conv_pool_pair_kernel<32, 64, ACTA, ACTB>), dim3((unsigned)a.n), dim3(kPairThreads), (unsigned)lds, s, x,
+            WA, WB, a, b, ea, eb, clear);
+}
+
+void launch_conv_pool_pair(const float* x, const int8_t* WA, const int8_t* WB, const ConvShape& a, const ConvShape& b,
+                           const Epilogue& ea, const Epilogue& eb, SlotClear clear, hipStream_t s) {
+  const bool acts_ok = (ea.act == rgmath::ACT_RELU || ea.act == rgmath::ACT_NONE) &&
+                       (eb.act == rgmath::ACT_RELU || eb.act == rgmath::ACT_NONE);
+  if (!conv_pool_pair_supported(a, b) || !acts_ok || ea.pool2 != 2 || eb.pool2 != 1 || !ea.absmax_in ||
+      !eb.absmax_in || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(WA) & 15) ||
+      (reinterpret_cast<uintptr_t>(WB) & 15))
+    throw std::logic_error("conv pair: the two convs do not fit the one-image kernel");
+  const bool ra = ea.act == rgmath::ACT_RELU, rb = eb.act == rgmath::ACT_RELU;
+  if (ra && rb)
+    launch_pair_t<rgmath::ACT_RELU, rgmath::ACT_RELU>(x, WA, WB, a, b, ea, eb, clear, s);
+  else if (ra)
+    launch_pair_t<rgmath::ACT_RELU, rgmath::ACT_NONE>(x, WA, WB, a, b, ea, eb, clear, s);
+  else if (rb)
+    launch_pair_t<rgmath::ACT_NONE, rgmath::ACT_RELU>(x, WA, WB, a, b, ea, eb, clear, s);
+  else
+    launch_pair_t<rgmath::ACT_NONE, rgmath::ACT_NONE>(x, WA, WB, a, b, ea, eb, clear, s);
 }
 
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep, hipStream_t s) {

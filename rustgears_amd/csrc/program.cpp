@@ -157,6 +157,12 @@ struct OpPlan {
   int pool_r16 = 0;
   int pool_act = 0;  // FP32: the activation of the Act op it absorbs
   bool pool_fused = false;
+  // INT8 conv + pool, conv + pool on one image per workgroup
+  // (launch_conv_pool_pair): 1 on the first conv, which launches it, 2 on
+  // the second, which launches nothing; no_out on the first pool, whose
+  // output stays in LDS.
+  int pair = 0;
+  bool no_out = false;
 };
 
 struct Plan {
@@ -882,6 +888,28 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     }
     plan->tiny = tiny && wbytes <= kTinyWeightBytes;
   }
+  // Two INT8 conv + pool stages, the first on the run's input (it measures
+  // its images' absmax itself), run as one kernel per image when their shapes
+  // fit it; not in capture plans, which store every op's operand and output.
+  // RGNPU_CONV_PAIR=0 turns it off.
+  {
+    const char* ce = getenv("RGNPU_CONV_PAIR");
+    const bool on = P->precision == RGNPU_PRECISION_INT8 && !plan->capture && !(ce && atoi(ce) == 0);
+    for (size_t i = 0; on && i + 3 < nops; i++) {
+      OpPlan &a = plan->ops[i], &b = plan->ops[i + 2];
+      if (P->ops[i]->kind != OP_CONV || P->ops[i + 2]->kind != OP_CONV || a.pool_r16 != 2 || b.pool_r16 != 1 ||
+          !plan->ops[i + 1].pool_fused || !plan->ops[i + 3].pool_fused || P->ops[i + 1]->kind != OP_POOL ||
+          P->ops[i + 3]->kind != OP_POOL)
+        continue;
+      if (!a.explicit_absmax || !a.full_cov || !conv_self_absmax_supported(a.cs) || b.explicit_absmax ||
+          !conv_pool_pair_supported(a.cs, b.cs))
+        continue;
+      a.pair = 1;
+      b.pair = 2;
+      plan->ops[i + 1].no_out = true;
+      break;
+    }
+  }
   // Requantization fused into the producing GEMM: an INT8 Linear on the
   // unsplit MFMA GEMM whose next computing op is a Linear reading the same
   // rows (its absmax is this op's emitted slot).  Its barrier words join the
@@ -1419,8 +1447,37 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           }
           break;
         }
+        if (pl.pair == 2) {  // run by the first conv of the pair
+          pre = launch_events_used();
+          break;
+        }
         uint32_t* sl = slots + pl.slot_base;
         const int64_t per = c.C * c.H * c.W;
+        if (pl.pair == 1) {
+          const Op& ob = *P->ops[i + 2];
+          const OpPlan &pb = plan.ops[i + 2], &pool_b = plan.ops[i + 3];
+          Epilogue ea, eb;
+          ea.bias = op.d_bias.as<float>();
+          ea.act = op.act;
+          ea.act_param = op.act_param;
+          ea.absmax_in = sl;
+          ea.w_scale = op.w_scale;
+          ea.pool2 = pl.pool_r16;
+          eb.bias = ob.d_bias.as<float>();
+          eb.act = ob.act;
+          eb.act_param = ob.act_param;
+          eb.absmax_in = slots + pb.slot_base;
+          eb.w_scale = ob.w_scale;
+          eb.y = buf(pb.out_buf);
+          eb.y_stream = pb.out_buf == BUF_OUTPUT;
+          eb.pool2 = pb.pool_r16;
+          eb.absmax_out = pool_b.emit_slot >= 0 ? slots + pool_b.emit_slot : nullptr;
+          eb.absmax_out_per_image = pool_b.emit_per_image;
+          pre = launch_events_used();
+          launch_conv_pool_pair(in, op.d_w.as<int8_t>(), ob.d_w.as<int8_t>(), c, pb.cs, ea, eb, clear, s);
+          first_launched();
+          break;
+        }
         // a small, fully covered first image: the conv measures its absmax itself
         const bool self_absmax = pl.explicit_absmax && pl.full_cov && conv_self_absmax_supported(c);
         if (pl.explicit_absmax && !self_absmax) {
@@ -1524,9 +1581,10 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
       // pools in its epilogue (its buffer then holds the pool's output, which
       // is the output of the MaxPool2d op; an FP32 conv's absorbed Act op
       // likewise has none of its own), or the program runs as one tiny
-      // kernel (only the last op's output leaves its LDS).
+      // kernel (only the last op's output leaves its LDS), or the pool is
+      // the first of a conv pair's (its output stays in LDS).
       const bool has_out = !pl.requant && !pl.handoff && !pl.pool_r16 && !(pl.pool_fused && op.kind != OP_POOL) &&
-                           !(plan.tiny && pl.out_buf != BUF_OUTPUT);
+                           !(plan.tiny && pl.out_buf != BUF_OUTPUT) && !pl.no_out;
       plan.tap_out_ok[i] = has_out;
       if (has_out && pl.out_len > 0)
         RG_HIP(hipMemcpyAsync(plan.cap_out[i]->p, buf(pl.out_buf), (size_t)pl.out_len * sizeof(float),

@@ -253,6 +253,16 @@ struct ConvShape {
 };
 inline int64_t conv_cp(int64_t C) { return C <= 4 ? 4 : round_up(C, 16); }
 inline int64_t conv_kpad(int64_t C, int64_t k) { return round_up(k * k * conv_cp(C), 64); }
+// Two INT8 conv + MaxPool2d(2, 2) stages in one launch, one workgroup per
+// image (kernels.hip conv_pool_pair_kernel): conv A on 32 x 32 images with
+// at most 4 channels -> 32, 3 x 3, stride 1, pad 1, then conv B 32 -> 64 with
+// the same window, each with ReLU or no activation.  The first conv measures
+// its image's absmax itself and writes its key to ea.absmax_in[b]; conv B's
+// per-image absmax (over the pooled conv A output) goes to eb.absmax_in[b];
+// the pooled conv B output goes to eb.y and its absmax to eb.absmax_out.
+bool conv_pool_pair_supported(const ConvShape& a, const ConvShape& b);
+void launch_conv_pool_pair(const float* x, const int8_t* WA, const int8_t* WB, const ConvShape& a, const ConvShape& b,
+                           const Epilogue& ea, const Epilogue& eb, SlotClear clear, hipStream_t s);
 void launch_conv(const int8_t* xq, const int8_t* Wq, const ConvShape& cs, const Epilogue& ep,
                  hipStream_t s);
 // The same conv reading the f32 image and quantizing its band in LDS with

@@ -12,8 +12,9 @@ exists in memory after each op:
   GELU producers;
 * the scale every quantizing op derived from its absmax slot (per tensor for
   a Linear, per image for a conv, npu.rs:346-351);
-* the f32 output of every op that stores one (the conv + pool kernel stores
-  only the pooled output: the MaxPool2d op's).
+* the f32 output of every op that stores one (a conv + pool kernel stores
+  only the pooled output, the MaxPool2d op's; the CNN's two conv + pool
+  stages run as one kernel that keeps the first pool's output in LDS).
 
 Each is compared bit for bit with the oracle's capture of the same op, at
 the benchmark's full sizes: the 4 x 4096^2 GELU stack (8192 rows), the deep
@@ -89,11 +90,13 @@ def test_deep_mlp_production_operands(rg, ref):
 
 
 def test_cnn_production_operands(rg, ref):
-    """C: both convs quantize their f32 input into LDS and pool in their
-    epilogue (no i8 image, no conv output in memory: the MaxPool2d ops hold
-    the pooled outputs); the per-image scales come from conv1's own absmax
-    and from pool 1's fused absmax; the fc layer's operand comes from
-    quant_rows with pool 2's absmax, the head quantizes as it reads."""
+    """C: both convs run as one kernel per image (conv_pool_pair_kernel):
+    conv1 quantizes its f32 image into LDS, pools into LDS, and conv2
+    quantizes those pooled planes and pools into memory, so neither conv's
+    output nor pool 1's is in memory (pool 2's is); the per-image scales come
+    from conv1's own absmax and from the pooled planes' absmax, both written
+    to the convs' slots; the fc layer's operand comes from quant_rows with
+    pool 2's absmax, the head quantizes as it reads."""
     from rustgears_amd import configs
     model, x = configs.cnn()
     layers = model.export()
@@ -104,4 +107,4 @@ def test_cnn_production_operands(rg, ref):
     assert [l.split("(")[0] for l in labels] == ["NPU::FusedConv2dAct", "NPU::MaxPool2d", "NPU::FusedConv2dAct",
                                                  "NPU::MaxPool2d", "NPU::Flatten", "NPU::FusedGemmAct",
                                                  "NPU::Gemm"], labels
-    _check_production(rg, ref, layers, x, "cnn", [5], [1, 3, 4, 5, 6])
+    _check_production(rg, ref, layers, x, "cnn", [5], [3, 4, 5, 6])
