@@ -2011,6 +2011,244 @@ void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N
 }
 
 // ---------------------------------------------------------------------------
+// INT8 Linear with few output tiles (C's 4096 -> 256 on 256 images): instead
+// of quantizing the input in a pass of its own, running a few 128 x 128 tiles
+// (K split over more workgroups, the slices added by another kernel), one
+// workgroup of 16 waves owns a 16 x TN output block (TN 16 or 64) and a
+// slice of K (usually all of it).
+//  * Its waves take the slice's K steps of 64 (wave, wave + 16, ...), R at
+//    a time.  Per step a lane loads 16 f32 inputs of row l % 16 as four
+//    16-byte loads at K 16 g + 4 (l / 16) (g = 0..3), so that each load
+//    instruction reads 64 contiguous bytes of each of the 16 rows, and
+//    quantizes them as quant_rows_kernel does (QuantTensor::from_f32 with
+//    the producer's absmax, quantize.rs:18-24; quantize_rz_bounded, since
+//    the scale comes from the absmax of these very values).  A 4 x 4
+//    transpose over the lane quads (v_permlane32_swap, v_permlane16_swap)
+//    then gives lane l the K bytes [16 (l / 16), +16) of its row, the
+//    v_mfma_i32_16x16x64_i8 operand layout, and the weight rows are loaded
+//    in that layout directly.  The first round's loads are issued before
+//    the scale is folded from its slot, so the two round trips overlap.
+//  * The waves' exact i32 sums are added in LDS (integer addition: any
+//    order gives the same sum), one output per thread.
+//  * With one slice the thread applies the fused epilogue of the large GEMM
+//    (quantize.rs:104-113), stores y and raises the next op's absmax.  With
+//    S slices (few blocks and a long K) each thread adds its sum to its
+//    output's 64-bit word in acc (zero at the start of the run) with one
+//    device-scope atomic that returns the word's old value: the word's high
+//    bits count the slices added, its low 40 bits the sums plus 2^31 each
+//    (every term in [0, 2^32), so S <= 16 of them cannot carry into the
+//    count), and the thread whose slice completes the count applies the
+//    epilogue to the full sum.  No workgroup waits for another, and the
+//    slices' sums meet in one atomic round trip, with no fence (on this GPU
+//    an agent-scope fence writes back or invalidates the XCD's whole L2).
+// Inputs past K and rows past M read zeros (buffer loads with the input's
+// extent as their limit).  Workgroups are numbered so that the 8 XCDs each
+// take a contiguous run of (slice, block) pairs: the blocks of one row strip
+// and slice, which read the same inputs, share an XCD's L2.
+// ---------------------------------------------------------------------------
+namespace xqs {
+constexpr int kWaves = 16, kThreads = kWaves * 64, kTM = 16;
+constexpr int kMaxBlocks = 512, kTargetGrid = 256, kMaxSlices = 16;
+}  // namespace xqs
+
+// Dword g of lane quad q (lanes 16 q .. 16 q + 15) <-> dword q of lane quad g.
+__device__ __forceinline__ void quad_transpose(v4i& d) {
+  const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)d[0], (uint32_t)d[2], false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap((uint32_t)d[1], (uint32_t)d[3], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto e = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  d = v4i{(int32_t)c[0], (int32_t)c[1], (int32_t)e[0], (int32_t)e[1]};
+}
+
+template <int TN, int R>
+__global__ __launch_bounds__(xqs::kThreads) void gemm_xq_small_kernel(
+    const float* __restrict__ x, const int8_t* __restrict__ B, int M, int N, int xk, int Kpad, int tiles_m,
+    int tiles_n, int ks, Epilogue ep, uint64_t* __restrict__ acc64) {
+  using namespace xqs;
+  constexpr int NB = TN / 16, LD = TN + 4, OUT = kTM * TN;  // LD: the 4 lane quads' rows in different banks
+  static_assert(OUT <= kThreads, "one output per thread");
+  __shared__ int32_t red[kWaves * kTM * LD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = (int)gridDim.x, tiles = tiles_m * tiles_n, S = G / tiles;
+  int t = (int)blockIdx.x;
+  if ((G & 7) == 0) t = (t & 7) * (G >> 3) + (t >> 3);
+  const int z = t / tiles, tile = t - z * tiles;
+  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  const int m0 = tm * kTM, n0 = tn * TN;
+  const int rows = min(kTM, M - m0);
+  const uint32_t part = tensor_absmax_part(ep.absmax_in);
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x + (int64_t)m0 * xk), 0, (int)((uint32_t)(rows * xk) * 4u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(B + (int64_t)n0 * Kpad), 0, TN * Kpad, 0x00020000);
+  const int r = lane & 15, q = lane >> 4;
+  const uint32_t aoff = (uint32_t)(r * xk) * 4u + (uint32_t)q * 16u, boff = (uint32_t)(r * Kpad + q * 16);
+  const int nk = Kpad / 64, kb = z * ks, ke = min(nk, kb + ks);
+  v4i acc[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) acc[j] = v4i{0, 0, 0, 0};
+  v4f af[R][4];
+  v4i bf[R][NB];
+  auto load_round = [&](int s0) {
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      const int s = s0 + u * kWaves, k0 = s * 64;
+      if (s >= ke) break;  // wave-uniform
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        af[u][g] = __builtin_bit_cast(
+            v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                     ra, (int)(k0 + 16 * g + 4 * q < xk ? aoff + (uint32_t)(k0 + 16 * g) * 4u : kDropOffset), 0, 0));
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+        bf[u][j] = __builtin_bit_cast(
+            v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(boff + (uint32_t)(j * 16 * Kpad + k0)), 0, 0));
+    }
+  };
+  auto mma_round = [&](int s0, float inv) {
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+      if (s0 + u * kWaves >= ke) break;
+      v4i av;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][0] * inv);
+        const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][1] * inv);
+        const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][2] * inv);
+        const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][3] * inv);
+        const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u), hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+        av[g] = (int32_t)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      }
+      quad_transpose(av);
+#pragma unroll
+      for (int j = 0; j < NB; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bf[u][j], acc[j], 0, 0, 0);
+    }
+  };
+  int s0 = kb + wave;
+  load_round(s0);
+  const float sa = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
+  const float inv = 1.0f / sa;
+  mma_round(s0, inv);
+  for (s0 += kWaves * R; s0 < ke; s0 += kWaves * R) {
+    load_round(s0);
+    mma_round(s0, inv);
+  }
+  // result register i of lane l: D[4 (l / 16) + i][l % 16] of block j
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave * (kTM * LD) + (4 * q + i) * LD + j * 16 + r] = acc[j][i];
+  __syncthreads();
+  const int orow = tid / TN, ocol = tid % TN;
+  const bool mine = tid < OUT;
+  int32_t sum = 0;
+  if (mine) {
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) sum += red[w * (kTM * LD) + orow * LD + ocol];
+  }
+  bool done = mine;
+  if (S > 1 && mine) {
+    constexpr uint64_t kLow = (uint64_t(1) << 40) - 1;
+    const uint64_t add = (uint64_t(1) << 40) + (uint64_t)((int64_t)sum + (int64_t(1) << 31));
+    const uint64_t old =
+        __hip_atomic_fetch_add(acc64 + (int64_t)tile * OUT + tid, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    done = (old >> 40) == (uint64_t)(S - 1);
+    // the low 32 bits of sum(terms) - S 2^31: the i32 sum, wrapped as i32 accumulation wraps
+    sum = (int32_t)(uint32_t)((old & kLow) + (add & kLow) - ((uint64_t)S << 31));
+  }
+  uint32_t amax = 0;
+  const int row = m0 + orow, col = n0 + ocol;
+  if (done && row < M && col < N) {
+    const float cs = sa * ep.w_scale, b = ep.bias[col];
+    float v;
+    switch (ep.act) {
+      case rgmath::ACT_RELU: v = epi_value<rgmath::ACT_RELU>(sum, cs, b, ep.act_param); break;
+      case rgmath::ACT_SIGMOID: v = epi_value<rgmath::ACT_SIGMOID>(sum, cs, b, ep.act_param); break;
+      case rgmath::ACT_TANH: v = epi_value<rgmath::ACT_TANH>(sum, cs, b, ep.act_param); break;
+      case rgmath::ACT_GELU: v = epi_value<rgmath::ACT_GELU>(sum, cs, b, ep.act_param); break;
+      case rgmath::ACT_LEAKY_RELU: v = epi_value<rgmath::ACT_LEAKY_RELU>(sum, cs, b, ep.act_param); break;
+      case rgmath::ACT_SILU: v = epi_value<rgmath::ACT_SILU>(sum, cs, b, ep.act_param); break;
+      default: v = epi_value<rgmath::ACT_NONE>(sum, cs, b, ep.act_param); break;
+    }
+    ep.y[(int64_t)row * N + col] = v;
+    amax = rgmath::absmax_key(v);
+  }
+  if (ep.absmax_out) {
+    amax = wave_max_u32(amax);
+    if (lane == 0) spread_max(ep.absmax_out, amax);
+  }
+}
+
+// Block width (16 or 64), blocks and K slices: a workgroup's loads are
+// bound by the latency of its CU's outstanding misses, so the choice
+// minimises the bytes one CU loads -- per workgroup the slice's K steps times
+// 64 bytes times (16 rows x 4 bytes of input + TN weight rows), times the
+// workgroups per CU -- plus a charge for the slices' atomic round trip.  At
+// most kMaxSlices slices and kMaxBlocks blocks.  RGNPU_XQS_TN (16 or 64) and
+// RGNPU_XQS_SLICES (a power of two) force a geometry (measurement aids).
+struct XqsGeom {
+  int TN, tiles_m, tiles_n, S, ks;
+};
+static XqsGeom xqs_geom(int64_t M, int64_t Npad, int64_t Kpad) {
+  const int tiles_m = (int)((M + xqs::kTM - 1) / xqs::kTM), nk = (int)(Kpad / 64);
+  int force_tn = 0, force_s = 0;
+  if (const char* e = getenv("RGNPU_XQS_TN")) force_tn = atoi(e);
+  if (const char* e = getenv("RGNPU_XQS_SLICES")) force_s = atoi(e);
+  XqsGeom best{0, tiles_m, 0, 0, 0};
+  double best_cost = 0.0;
+  for (int TN : {16, 64}) {
+    if ((force_tn == 16 || force_tn == 64) && TN != force_tn) continue;
+    const int tiles_n = (int)(Npad / TN);
+    const int64_t tiles = (int64_t)tiles_m * tiles_n;
+    if (tiles > xqs::kMaxBlocks) continue;
+    for (int S = 1; S <= xqs::kMaxSlices; S *= 2) {
+      if (force_s > 0 && S != std::min(force_s, xqs::kMaxSlices)) continue;
+      const int ks = (nk + S - 1) / S, Se = (nk + ks - 1) / ks;
+      if (Se != S && S > 1) continue;  // fewer K steps than slices
+      const int64_t wgs = tiles * S, per_cu = (wgs + xqs::kTargetGrid - 1) / xqs::kTargetGrid;
+      const double cost = (double)per_cu * ks * 64.0 * (xqs::kTM * 4 + TN) + (S > 1 ? 32768.0 + 4096.0 * S : 0.0);
+      if (best.TN == 0 || cost < best_cost) {
+        best = XqsGeom{TN, tiles_m, tiles_n, S, ks};
+        best_cost = cost;
+      }
+    }
+  }
+  if (best.TN == 0) best = XqsGeom{64, tiles_m, (int)(Npad / 64), 1, nk};
+  return best;
+}
+
+bool gemm_xq_small_supported(int64_t M, int64_t N, int64_t Npad, int64_t K, int64_t Kpad) {
+  if (!(M > 0 && M < (int64_t(1) << 30) && N > 0 && N <= Npad && Npad % 64 == 0 && K > 0 && K % 4 == 0 &&
+        K <= Kpad && Kpad % 64 == 0 && Kpad * 64 < (int64_t(1) << 31) && K * xqs::kTM * 4 < (int64_t(1) << 31)))
+    return false;
+  const XqsGeom g = xqs_geom(M, Npad, Kpad);
+  return (int64_t)g.tiles_m * g.tiles_n <= xqs::kMaxBlocks;
+}
+
+int64_t gemm_xq_small_sync_words(int64_t M, int64_t Npad, int64_t Kpad) {
+  const XqsGeom g = xqs_geom(M, Npad, Kpad);
+  return g.S > 1 ? (int64_t)g.tiles_m * g.tiles_n * xqs::kTM * g.TN * 2 : 0;
+}
+
+void launch_gemm_xq_small(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t K,
+                          int64_t Kpad, const Epilogue& ep, uint32_t* sync, hipStream_t s) {
+  if (!gemm_xq_small_supported(M, N, Npad, K, Kpad) || (reinterpret_cast<uintptr_t>(x) & 15) || !ep.absmax_in ||
+      ep.acc_out || ep.h_out || ep.pool2)
+    throw std::logic_error("small GEMM: unsupported shape, unaligned input, no slot or capture outputs");
+  const XqsGeom g = xqs_geom(M, Npad, Kpad);
+  if (g.S > 1 && (!sync || (reinterpret_cast<uintptr_t>(sync) & 7)))
+    throw std::logic_error("small GEMM: K slices need zeroed, 8-byte aligned sum words");
+  uint64_t* const acc64 = reinterpret_cast<uint64_t*>(sync);
+  const dim3 grid((unsigned)(g.S * g.tiles_m * g.tiles_n));
+  if (g.TN == 16)
+    RG_LAUNCH((gemm_xq_small_kernel<16, 4>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
+              (int)Kpad, g.tiles_m, g.tiles_n, g.ks, ep, acc64);
+  else
+    RG_LAUNCH((gemm_xq_small_kernel<64, 2>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
+              (int)Kpad, g.tiles_m, g.tiles_n, g.ks, ep, acc64);
+}
+
+// ---------------------------------------------------------------------------
 // A whole program of small INT8 Linears in one workgroup (npu.rs:307-318 op
 // after op).  The input, every layer's weights and biases are copied into LDS
 // by global_load_lds (every copy in flight at once, one memory round trip).

@@ -163,6 +163,10 @@ struct OpPlan {
   // output stays in LDS.
   int pair = 0;
   bool no_out = false;
+  // INT8 Linear with few output tiles reading its f32 input and quantizing
+  // it as it reads it (launch_gemm_xq_small): no quantize pass before it.
+  bool small_xq = false;
+  int64_t xq_sync_base = -1;  // its 64-bit sum words in the slot set (K slices), or -1
 };
 
 struct Plan {
@@ -984,6 +988,31 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     pl.iq_sync_base = round_up(slots, kSpreadStride);
     slots = pl.iq_sync_base + input_quant_sync_words(pl.Mpad, op.Kpad);
   }
+  // An INT8 Linear with fewer than 128 output tiles of 128 x 128 (the tile
+  // GEMM would split K or leave most CUs idle) whose input's absmax a
+  // producer emitted quantizes that input as it reads it, one workgroup per
+  // small output block and K slice: no quantize pass and no kernel adding
+  // the slices (they meet in one 64-bit word per output in the slot set).
+  // Not in capture plans, which store the i8 operand.  RGNPU_SMALL_XQ=0
+  // turns it off.
+  {
+    const char* xe = getenv("RGNPU_SMALL_XQ");
+    const bool on = P->precision == RGNPU_PRECISION_INT8 && !plan->capture && !plan->tiny && !(xe && atoi(xe) == 0);
+    for (size_t i = 0; on && i < nops; i++) {
+      const Op& op = *P->ops[i];
+      OpPlan& pl = plan->ops[i];
+      pl.small_xq = op.kind == OP_LINEAR && !pl.gemv && op.out_f > kNarrowMaxN && pl.rows > 0 &&
+                    !pl.explicit_absmax && !pl.q_ready && !pl.requant &&
+                    (pl.Mpad / 128) * (op.Npad / 128) < 128 &&
+                    gemm_xq_small_supported(pl.rows, op.out_f, op.Npad, op.in_f, op.Kpad);
+      if (!pl.small_xq) continue;
+      const int64_t words = gemm_xq_small_sync_words(pl.rows, op.Npad, op.Kpad);
+      if (words > 0) {
+        pl.xq_sync_base = round_up(slots, kSpreadStride);
+        slots = pl.xq_sync_base + words;
+      }
+    }
+  }
   if (const char* e = getenv("RGNPU_REQUANT_SPIN_LIMIT")) plan->spin_limit = std::max(0, atoi(e));
   else plan->spin_limit = 100000;  // x kBarrierPollUs (0.32 us) = ~32 ms
   if (const char* e = getenv("RGNPU_GELU_CERT")) plan->gelu_cert = std::min(3, std::max(0, atoi(e)));
@@ -1343,7 +1372,8 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         // A one-row GEMV quantizes its input itself, with the producer's
         // absmax or, when its input has none yet, the input's own.
         const bool gemv_xq = pl.gemv && !pl.q_ready && gemv_xq_supported(pl.rows, op.in_f, op.Kpad, in);
-        if (narrow_xq || gemv_xq) {
+        const bool small_xq = pl.small_xq && !cap && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+        if (narrow_xq || gemv_xq || small_xq) {
           // nothing before the GEMM
         } else if (pl.iq_sync_base >= 0) {
           launch_input_quant(in, pl.rows, op.K, pl.Mpad, op.Kpad, slot, qa, scales + pl.scale_base,
@@ -1388,6 +1418,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
             if (pl.explicit_absmax) first_launched();
           } else if (pl.gemv) {
             launch_gemv(qa, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.Kpad, ep, s);
+          } else if (small_xq) {
+            launch_gemm_xq_small(in, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.Npad, op.in_f, op.Kpad, ep,
+                                 pl.xq_sync_base >= 0 ? slots + pl.xq_sync_base : nullptr, s);
           } else if (narrow_xq) {
             launch_gemm_narrow_xq(in, op.d_w.as<int8_t>(), pl.rows, op.out_f, op.in_f, op.Kpad, ep, cap ? qa : nullptr,
                                   cap ? scales + pl.scale_base : nullptr, s);
@@ -1399,9 +1432,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
           }
         }
         if (cap) RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, qa, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
-        // the one-row GEMV and the narrow GEMM that quantize as they read
-        // leave no i8 operand in memory
-        if (tap && pl.rows > 0 && !narrow_xq && !gemv_xq) {
+        // the one-row GEMV and the narrow and small GEMMs that quantize as
+        // they read leave no i8 operand in memory
+        if (tap && pl.rows > 0 && !narrow_xq && !gemv_xq && !small_xq) {
           RG_HIP(hipMemcpyAsync(plan.cap_q[i]->p, qa, (size_t)(pl.Mpad * op.Kpad), hipMemcpyDeviceToDevice, s));
           plan.tap_q_ok[i] = 1;
         }

@@ -196,6 +196,18 @@ void launch_gemm_narrow(const int8_t* A, const int8_t* B, int64_t M, int64_t N, 
 bool gemm_narrow_xq_supported(int64_t K, int64_t Kpad);
 void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t K, int64_t Kpad,
                            const Epilogue& ep, int8_t* q_out, float* scale_out, hipStream_t s);
+// INT8 Linear with few output tiles, reading the f32 input x [M, K] and
+// quantizing it as it is read with the scale of the spread slot
+// ep.absmax_in: one workgroup per 16 x 16 or 16 x 64 output block and K
+// slice, the slice's K steps spread over its waves and their sums added in
+// LDS; the fused epilogue of launch_gemm.  B [Npad, Kpad].  With more than
+// one K slice, sync (gemm_xq_small_sync_words, zero at launch, 8-byte
+// aligned) holds a 64-bit word per output in which the slices meet.  No
+// capture outputs.
+bool gemm_xq_small_supported(int64_t M, int64_t N, int64_t Npad, int64_t K, int64_t Kpad);
+int64_t gemm_xq_small_sync_words(int64_t M, int64_t Npad, int64_t Kpad);
+void launch_gemm_xq_small(const float* x, const int8_t* B, int64_t M, int64_t N, int64_t Npad, int64_t K,
+                          int64_t Kpad, const Epilogue& ep, uint32_t* sync, hipStream_t s);
 // A whole program of small INT8 Linears (npu.rs:307-318 per op: the input
 // quantized per tensor with its own absmax, quantize.rs:18-24, then the
 // fused GEMM, quantize.rs:93-118) in one workgroup, for programs whose every
