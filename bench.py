@@ -137,11 +137,23 @@ def dominant_roofline(name, records, layers, x, workload, prec="int8"):
         return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(workload, r.op, prec, occ), "kernel": r.op,
                 "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_bytes": byts}, best
-    ops = 2 * r.macs
+    # ops that launch nothing after it ran inside its kernel (the second conv
+    # of a conv pair, the later Linears of a whole-program kernel)
+    macs, fused = r.macs, []
+    for rr in records[best + 1:]:
+        if rr.kernel_ns > 0:
+            break
+        if rr.macs > 0:
+            macs += rr.macs
+            fused.append(rr.op)
+    ops = 2 * macs
     ach = ops / secs / 1e12
-    return {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-            "frac": round(ach / peak, 4), "traffic": measured_traffic(workload, r.op, prec, occ), "kernel": r.op,
-            "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}, best
+    out = {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+           "frac": round(ach / peak, 4), "traffic": measured_traffic(workload, r.op, prec, occ), "kernel": r.op,
+           "kernel_us": round(r.kernel_ns / 1e3, 2), "algorithmic_ops": ops}
+    if fused:
+        out["fused_ops"] = fused
+    return out, best
 
 
 def host_description() -> dict:
