@@ -1688,9 +1688,12 @@ void launch_gemv_xq(const float* x, const int8_t* B, int64_t N, int64_t Npad, in
 // The weights stream through LDS: an item is 16 weight rows x one 512-byte
 // K piece (8 KiB), copied by 8 global_load_lds instructions of two 512-byte
 // row pieces each, so every instruction reads whole 128-byte lines.  Each
-// wave owns a two-stage ring and streams its own items (no workgroup barrier
-// in the loop); the next item's copy is issued before the current one is
-// consumed.  v_mfma_i32_16x16x64_i8 takes the weights as A (row n = lane %
+// wave owns a three-stage ring and streams its own items (no workgroup
+// barrier in the loop): while it consumes item i the copies of items i + 1
+// and i + 2 are in flight.  A piece's activations (M <= 8 rows x 512 bytes)
+// travel the same way, into the stage of the piece's first item, so no
+// register is the target of a load in flight and the waits are exactly the
+// counted ones.  v_mfma_i32_16x16x64_i8 takes the weights as A (row n = lane %
 // 16) and the activations as B (column m = lane % 16, zero for m >= M), so
 // D[n][m] is the exact i32 sum; the activation fragments of a piece (8 K
 // steps x 16 bytes per lane) are loaded once per piece and serve every row
@@ -1711,11 +1714,15 @@ constexpr int kPiece = 512;                // K bytes per piece
 constexpr int kItem = 16 * kPiece;         // 16 rows x one piece
 constexpr int kDma = kItem / 1024;         // copy instructions per item
 constexpr int kSteps = kPiece / 64;        // MFMA K steps per piece
-constexpr int kRing = kWaves * 2 * kItem;  // 64 KiB
+constexpr int kXBytes = 8 * kPiece;             // a piece's activations, 8 rows
+constexpr int kXDma = kXBytes / 1024;           // their copy instructions
+constexpr int kStage = kItem + kXBytes;         // 12 KiB
+constexpr int kStages = 3;
+constexpr int kRing = kWaves * kStages * kStage;  // 144 KiB
 constexpr int kRedWords = kGmvBlocks * 16 * 8;
+constexpr int kLds = kRing + kRedWords * 4;
 // Past half of the CU's 160 KiB, so the grid spreads one workgroup per CU.
-constexpr int kLds = 96 * 1024;
-static_assert(kRing + kRedWords * 4 <= kLds, "LDS plan");
+static_assert(kLds > 80 * 1024 && kLds <= 160 * 1024, "LDS plan");
 }  // namespace gmv
 
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ B,
@@ -1732,58 +1739,74 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(const int8_t* __restrict
   for (int i = threadIdx.x; i < kRedWords; i += 256) red[i] = 0;
   __syncthreads();
 
-  int8_t* const ring = smem + wave * 2 * kItem;
+  int8_t* const ring = smem + wave * kStages * kStage;
   const int8_t* const wbase = B + (int64_t)bb * 16 * Kpad;
   const int drow = lane >> 5, dchunk = lane & 31;  // copy: two 512-byte row pieces per instruction
   const int r = lane & 15, q = lane >> 4;          // fragment: row / column r, K quarter q
-  const int8_t* const xrow = A + (int64_t)(r < M ? r : M - 1) * Kpad + q * 16;
-  v4i xs[kSteps], xc[kSteps], acc[kGmvBlocks];
+  v4i xc[kSteps], acc[kGmvBlocks];
 #pragma unroll
   for (int b = 0; b < kGmvBlocks; b++) acc[b] = v4i{0, 0, 0, 0};
-  // The activation fragments of piece p; issued with the piece's first item,
-  // so they land before its copies.
-  // (only lanes whose batch row exists load; the others use zeros)
-#pragma unroll
-  for (int s = 0; s < kSteps; s++) xs[s] = v4i{0, 0, 0, 0};
-  auto load_x = [&](int p) {
-    if (r < M) {
-#pragma unroll
-      for (int s = 0; s < kSteps; s++) xs[s] = *reinterpret_cast<const v4i*>(xrow + p * kPiece + s * 64);
-    }
-  };
-  // Item (p, b) into stage `stage`.
+  // Item (p, b) into stage `stage`: for b == 0 first the piece's activation
+  // rows (rows past M repeat row M - 1; their columns are never used), then
+  // the weights.  Row rr's chunk c lands at position c ^ rr.
   auto issue = [&](int p, int b, int stage) {
+    int8_t* dst = ring + stage * kStage;
+    if (b == 0) {
+#pragma unroll
+      for (int j = 0; j < kXDma; j++) {
+        const int rr = 2 * j + drow;
+        dma16(A + (int64_t)(rr < M ? rr : M - 1) * Kpad + p * kPiece + ((dchunk ^ rr) << 4),
+              dst + kItem + j * 1024);
+      }
+    }
     const int8_t* src = wbase + (int64_t)b * 16 * Kpad + p * kPiece;
-    int8_t* dst = ring + stage * kItem;
 #pragma unroll
     for (int j = 0; j < kDma; j++) {
       const int rr = 2 * j + drow;
       dma16(src + (int64_t)rr * Kpad + ((dchunk ^ rr) << 4), dst + j * 1024);
     }
   };
-  if (nitems > 0) {
-    load_x(p0);
-    issue(p0, 0, 0);
-  }
+  // Item k is (piece p0 + k / nbl, row block k % nbl) in stage k % kStages;
+  // two items are in flight ahead of the one consumed.
+  const int dist = 2;
+  int issued = 0, ip = p0, ib = 0;  // next item to issue and its (piece, block)
+  auto issue_next = [&]() {
+    issue(ip, ib, issued % kStages);
+    issued++;
+    if (++ib == nbl) {
+      ib = 0;
+      ip++;
+    }
+  };
+  while (issued < dist && issued < nitems) issue_next();
   int i = 0;
   for (int p = p0; p < p1; p++) {
 #pragma unroll
     for (int b = 0; b < kGmvBlocks; b++) {
       if (b < nbl) {
-        wait_vmcnt<0>();  // item i (and, at b == 0, the piece's activations) landed
-        if (b == 0) {
-#pragma unroll
-          for (int s = 0; s < kSteps; s++) xc[s] = r < M ? xs[s] : v4i{0, 0, 0, 0};
+        // Wait for item i: what was issued after it may stay in flight --
+        // item i + 1's weight copies (kDma) and, when that item starts a
+        // piece, its activation copies (kXDma).  Loads complete in order.
+        if (issued > i + 1) {
+          if (b + 1 == nbl)
+            wait_vmcnt<kDma + kXDma>();
+          else
+            wait_vmcnt<kDma>();
+        } else {
+          wait_vmcnt<0>();
         }
-        if (i + 1 < nitems) {
-          if (b + 1 == nbl) {
-            load_x(p + 1);
-            issue(p + 1, 0, (i + 1) & 1);
-          } else {
-            issue(p, b + 1, (i + 1) & 1);
+        const int8_t* const sb = ring + (i % kStages) * kStage;
+        if (b == 0) {
+          // the piece's activation fragments (zero for rows past M)
+          const int8_t* const xr = sb + kItem + (r < M ? r : 0) * kPiece;
+#pragma unroll
+          for (int s = 0; s < kSteps; s++) {
+            const v4i v = *reinterpret_cast<const v4i*>(xr + (((4 * s + q) ^ (r < M ? r : 0)) << 4));
+            xc[s] = r < M ? v : v4i{0, 0, 0, 0};
           }
         }
-        const int8_t* st = ring + (i & 1) * kItem + r * kPiece;
+        if (issued < nitems) issue_next();
+        const int8_t* st = sb + r * kPiece;
 #pragma unroll
         for (int s = 0; s < kSteps; s++) {
           const v4i wf = *reinterpret_cast<const v4i*>(st + (((4 * s + q) ^ r) << 4));
