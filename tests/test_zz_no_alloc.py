@@ -6,7 +6,9 @@ Through the C ABI, against rgnpu_program_run_device on the same program and
 input, bit for bit, on two calls in a row, the second with a smaller input;
 another program's allocation-free call between them leaves different data
 in the shared scratch.  Covered: INT8 Linear chains with the fused
-requantization (two i8 operand buffers, barrier words in the slots), an INT8
+requantization (two i8 operand buffers, barrier words in the slots), a
+Linear on the small-tile GEMM whose K slices meet in sum words of the slot
+set, an INT8
 conv net with partial window coverage (masks uploaded by every call), FP16
 convs with split K (workspace and the [n*L, O] staging buffer) and the FP32
 provider.  A shape whose buffers exceed the scratch is refused with
@@ -89,6 +91,26 @@ def test_noalloc_matches_run_device_mlp(rg, ref, prec):
     assert_bitexact_f32(d, c, f"other program {prec}")
     a, b = _both(rg, sess, x2, f"mlp {prec} 40 rows")
     assert_bitexact_f32(b, a, f"mlp {prec} 40 rows (second, smaller)")
+    sess.close()
+    sess2.close()
+
+
+def test_noalloc_small_gemm_k_slices(rg, ref):
+    """A Linear on the small-tile GEMM with K slices (4096 -> 256 at 16 and
+    12 rows: eight slices meeting in 64-bit sum words in the slot set, which
+    every allocation-free call zeroes in the shared scratch)."""
+    from rustgears_amd import nn
+    layers = _mlp(rg, [1024, 4096, 256], nn.Relu, seed=12)
+    other = _mlp(rg, [96, 200, 64], nn.Gelu, seed=6)
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    sess2 = rg.InferenceSession.from_layers(other, rg.ExecutionProvider.mi355x_int8())
+    for rows in (16, 12):
+        x = rg.randn([rows, 1024])
+        a, b = _both(rg, sess, x, f"k slices {rows} rows")
+        assert_bitexact_f32(b, a, f"k slices {rows} rows")
+        assert_bitexact_f32(b, ref.RefProgram(layers).run(x, parallel=True), f"k slices {rows} rows vs oracle")
+        c, d = _both(rg, sess2, rg.randn([700, 96]), "other program")
+        assert_bitexact_f32(d, c, "other program")
     sess.close()
     sess2.close()
 
