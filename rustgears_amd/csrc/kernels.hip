@@ -2610,12 +2610,18 @@ __device__ __forceinline__ void conv_band_epilogue(const v4i (&acc)[TM / 16][TN 
 // absmax for the next op is over the pooled values.  LDS: the pooled values
 // go to the image's planes lout [O, OH/2, OW/2] in LDS instead, and the
 // block's absmax is left to the caller (the lane's key is returned).
+// With ReLU the window is pooled on the i32 sums: relu(fl(fl(s * csc) + b))
+// is non-decreasing in s for every scale product csc the reference can
+// form (positive, +inf, or NaN, where every value is +0), and ReLU leaves
+// no NaN and no -0, so the largest value of the window is the value of its
+// largest sum, bit for bit, and one epilogue evaluation serves four outputs.
 
-template <int TM, int TN, int ACT, int R16, bool LDS = false, int NW = 4>
+template <int TM, int TN, int ACT, int R16, bool LDS = false, int NW = 4, bool LBIAS = false>
 __device__ __forceinline__ uint32_t conv_band_epilogue_pool2(const v4i (&acc)[TM / 16][TN / 64], const ConvShape& cs,
                                                              const Epilogue& ep, int b, int o0,
                                                              const int (&pix)[TN / 64], float csc, int lane,
-                                                             uint32_t* red, float* lout = nullptr) {
+                                                             uint32_t* red, float* lout = nullptr,
+                                                             const float* lbias = nullptr) {
   constexpr int FM = TM / 16, FN = TN / 64;
   static_assert(FN % (2 * R16) == 0, "a wave's pixels are whole pairs of output rows");
   const int O = (int)cs.O;
@@ -2626,9 +2632,13 @@ __device__ __forceinline__ uint32_t conv_band_epilogue_pool2(const v4i (&acc)[TM
   // through a bounded resource over the image's pooled planes with 32-bit
   // offsets o * PL + pp (host-checked: O * PL * 4 < 2^31)
   const __amdgpu_buffer_rsrc_t ry = bounded_rsrc(LDS ? nullptr : ep.y + (int64_t)b * O * PL);
-  float4 b4[FM];  // the lane's 4 output channels of each row block (bias padded to Opad)
+  // the lane's 4 output channels of each row block (bias padded to Opad;
+  // LBIAS: a copy in LDS, staged before the K loop, so no global load sits
+  // between the MFMAs and the stores)
+  float4 b4[FM];
 #pragma unroll
-  for (int i = 0; i < FM; i++) b4[i] = *reinterpret_cast<const float4*>(ep.bias + o0 + i * 16 + (lane >> 4) * 4);
+  for (int i = 0; i < FM; i++)
+    b4[i] = *reinterpret_cast<const float4*>((LBIAS ? lbias : ep.bias) + o0 + i * 16 + (lane >> 4) * 4);
   int pp[FN];
   const uint32_t owmag = div_magic((uint32_t)OW);
 #pragma unroll
@@ -2638,6 +2648,35 @@ __device__ __forceinline__ uint32_t conv_band_epilogue_pool2(const v4i (&acc)[TM
     pp[j] = (even && p < L) ? (oy >> 1) * POW + (ox >> 1) : -1;
   }
   uint32_t amax = 0;
+  if constexpr (ACT == rgmath::ACT_RELU) {
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int o = o0 + i * 16 + (lane >> 4) * 4 + r;
+        int32_t h[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) h[j] = dpp_partner<1>(acc[i][j][r]);  // lane ^ 1
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+          if ((j / R16) % 2 != 0) continue;
+          const int jn = j + R16 < FN ? j + R16 : j;
+          const int32_t mx = max(max(acc[i][j][r], h[j]), max(acc[i][jn][r], h[jn]));
+          const float best = epi_value<ACT>(mx, csc, b4[i][r], ep.act_param);
+          const bool ok = pp[j] >= 0 && o < O;
+          if constexpr (LDS) {
+            if (ok) lout[o * PL + pp[j]] = best;
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, best), ry,
+                                                  (int)(ok ? (uint32_t)(o * PL + pp[j]) * 4u : kDropOffset), 0, 0);
+          }
+          const uint32_t key = ok ? rgmath::fbits(best) : 0u;
+          amax = key > amax ? key : amax;
+        }
+      }
+    if constexpr (!LDS) conv_block_absmax<NW>(ep, b, amax, red, lane);
+    return amax;
+  }
 #pragma unroll
   for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -2734,6 +2773,56 @@ __device__ __forceinline__ void conv_band_mma(const int8_t* wts, const int8_t* b
           const int8_t* a = (rowoff[j] >= 0 && tap < kk) ? band + rowoff[j] + toff : zero16;
           bf[j][e] = *reinterpret_cast<const int*>(a);
         }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// conv_band_mma with every dimension known at compile time and every pixel
+// of the block inside the output, oy0 = 0 and stride 1 (the pair kernel's
+// two convs): the divisions, the tap offsets and the K loop fold to
+// constants and immediates.
+template <int TM, int TN, bool CP4, int OW, int WP, int CP, int K, int KP, int WSTRIDE>
+__device__ __forceinline__ void conv_band_mma_fixed(const int8_t* wts, const int8_t* band, const int8_t* zero16, int p0,
+                                                    int wave, int lane, int (&pix)[TN / 64],
+                                                    v4i (&acc)[TM / 16][TN / 64]) {
+  constexpr int WTN = TN / 4, FM = TM / 16, FN = WTN / 16, KK = K * K;
+  static_assert(KP % 64 == 0 && (OW & (OW - 1)) == 0, "whole K steps; a power-of-two row");
+  int rowoff[FN];
+#pragma unroll
+  for (int j = 0; j < FN; j++) {
+    pix[j] = p0 + wave * WTN + j * 16 + (lane & 15);
+    rowoff[j] = ((pix[j] / OW) * WP + pix[j] % OW) * CP;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; i++)
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+  const int q16 = (lane >> 4) * 16;  // this lane's 16-byte K chunk within a step
+#pragma unroll
+  for (int k0 = 0; k0 < KP; k0 += 64) {
+    const int kb = k0 + q16;
+    v4i af[FM], bf[FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(wts + (i * 16 + (lane & 15)) * WSTRIDE + kb);
+    if constexpr (!CP4) {
+      const int tap = kb / CP, c0 = kb % CP;
+      const int toff = ((tap / K) * WP + tap % K) * CP + c0;
+#pragma unroll
+      for (int j = 0; j < FN; j++)
+        bf[j] = *reinterpret_cast<const v4i*>(tap < KK ? band + rowoff[j] + toff : zero16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int tap = (kb >> 2) + e;
+        const int toff = ((tap / K) * WP + tap % K) * 4;
+#pragma unroll
+        for (int j = 0; j < FN; j++) bf[j][e] = *reinterpret_cast<const int*>(tap < KK ? band + rowoff[j] + toff : zero16);
       }
     }
 #pragma unroll
@@ -3250,6 +3339,10 @@ static __host__ __device__ inline PairLds pair_lds(int OA, int OB, int KPA, int 
 }
 
 constexpr int kPairThreads = 1024;  // 16 waves: four groups of 4, four waves per SIMD
+// the two convs' K padding (conv_kpad: 9 taps x 4 channel bytes, 9 taps x 32)
+constexpr int kPairKpA = 64, kPairKpB = 320;
+// static LDS of the pair kernel (wave maxima, the two convs' biases) stays under this bound
+constexpr int kPairStaticLds = 512;
 constexpr int kPairWbUnits = 2;     // 16-byte weight units of conv B per thread at most (OB * KPB <= 2 * 1024 * 16)
 
 template <int OA, int OB, int ACTA, int ACTB>
@@ -3263,8 +3356,11 @@ __global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const floa
   static_assert(OA % 16 == 0 && OB % (16 * NG) == 0, "channel blocks of 16; conv B's channels split over the groups");
   extern __shared__ __attribute__((aligned(16))) int8_t dsm[];
   __shared__ uint32_t red[NW];
+  __shared__ __attribute__((aligned(16))) float lbias[OA + OB];  // both convs' biases
+  static_assert(sizeof(red) + sizeof(lbias) <= kPairStaticLds, "static LDS bound");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = wave >> 2, wl = wave & 3, b = blockIdx.x;
-  const int C = (int)csA.C, KPA = (int)csA.Kpad, KPB = (int)csB.Kpad;
+  const int C = (int)csA.C;
+  constexpr int KPA = kPairKpA, KPB = kPairKpB;  // host-checked against the shapes
   // the shapes with their sides as constants, so the epilogues' divisions fold
   ConvShape sa = csA, sb = csB;
   sa.O = OA;
@@ -3302,6 +3398,8 @@ __global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const floa
     const int i = tid + NT * t;
     wbv[t] = reinterpret_cast<const v4i*>(WB)[i < nb ? i : nb - 1];
   }
+  // the biases (padded to Opad), read with the image and weights
+  const float bv = tid < OA ? epA.bias[tid] : epB.bias[tid < OA + OB ? tid - OA : 0];
   // both bands and their zero blocks to zero (they are contiguous)
   for (int i = tid; i < (ly.plane - ly.band_a) / 16; i += NT) reinterpret_cast<v4i*>(band_a)[i] = v4i{0, 0, 0, 0};
   clear_slots(clear);
@@ -3317,6 +3415,7 @@ __global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const floa
       *reinterpret_cast<v4i*>(wb + row * (KPB + 16) + c16 * 16) = wbv[t];
     }
   }
+  if (tid < OA + OB) lbias[tid] = bv;
   // 1. the image's absmax (NaN ignored, like f32::max)
   float m = 0.0f;
 #pragma unroll
@@ -3350,15 +3449,15 @@ __global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const floa
   // 3. conv A, pooled into the planes: the wave groups take the 256-pixel
   // blocks in turn
   const float csc_a = scale_a * epA.w_scale;
-  const BandGeom ga{S, S * S, 0, 1, SA, 4, 3, 9, KPA, KPA + 16};
   uint32_t ma = 0;
 #pragma unroll 1
   for (int blk = grp; blk < (S * S) / 256; blk += NG) {
     int pix[4];
     v4i acc[OA / 16][4];
-    conv_band_mma<OA, 256, true>(wa, band_a, dsm + ly.zero_a, ga, blk * 256, wl, lane, pix, acc);
-    const uint32_t t = conv_band_epilogue_pool2<OA, 256, ACTA, 2, true>(acc, sa, epA, b, 0, pix, csc_a, lane, red,
-                                                                        plane);
+    conv_band_mma_fixed<OA, 256, true, S, SA, 4, 3, kPairKpA, kPairKpA + 16>(wa, band_a, dsm + ly.zero_a, blk * 256, wl,
+                                                                             lane, pix, acc);
+    const uint32_t t = conv_band_epilogue_pool2<OA, 256, ACTA, 2, true, 4, true>(acc, sa, epA, b, 0, pix, csc_a, lane,
+                                                                                 red, plane, lbias);
     ma = t > ma ? t : ma;
   }
   // 4. conv B's scale: the absmax of the pooled planes
@@ -3391,12 +3490,12 @@ __global__ __launch_bounds__(kPairThreads) void conv_pool_pair_kernel(const floa
   __syncthreads();
   // 6. conv B, pooled into y: each wave group takes OB / NG output channels
   constexpr int OH = OB / NG;
-  const BandGeom gb{PS, PL, 0, 1, SB, OA, 3, 9, KPB, KPB + 16};
   int pix[4];
   v4i acc[OH / 16][4];
-  conv_band_mma<OH, 256, false>(wb + grp * OH * (KPB + 16), band_b, dsm + ly.zero_b, gb, 0, wl, lane, pix, acc);
-  conv_band_epilogue_pool2<OH, 256, ACTB, 1, false, NW>(acc, sb, epB, b, grp * OH, pix, scale_b * epB.w_scale, lane,
-                                                        red);
+  conv_band_mma_fixed<OH, 256, false, PS, SB, OA, 3, kPairKpB, kPairKpB + 16>(wb + grp * OH * (kPairKpB + 16), band_b,
+                                                                              dsm + ly.zero_b, 0, wl, lane, pix, acc);
+  conv_band_epilogue_pool2<OH, 256, ACTB, 1, false, NW, true>(acc, sb, epB, b, grp * OH, pix, scale_b * epB.w_scale,
+                                                              lane, red, nullptr, lbias + OA);
 }
 
 bool conv_pool_pair_supported(const ConvShape& a, const ConvShape& b) {
@@ -3406,8 +3505,9 @@ bool conv_pool_pair_supported(const ConvShape& a, const ConvShape& b) {
   const bool ok_b = b.C == 32 && b.cp == 32 && b.H == S / 2 && b.W == S / 2 && b.k == 3 && b.stride == 1 &&
                     b.pad == 1 && b.OH == S / 2 && b.OW == S / 2 && b.O == 64 && b.Opad == 64 &&
                     b.Kpad == conv_kpad(32, 3) && b.n == a.n;
-  return ok_a && ok_b && a.n >= 1 && a.n <= 65535 && 64 * (b.Kpad / 16) <= kPairThreads * kPairWbUnits &&
-         pair_lds(32, 64, (int)a.Kpad, (int)b.Kpad).total <= 160 * 1024 - 64;
+  return ok_a && ok_b && a.Kpad == kPairKpA && b.Kpad == kPairKpB && a.n >= 1 && a.n <= 65535 &&
+         64 * (b.Kpad / 16) <= kPairThreads * kPairWbUnits &&
+         pair_lds(32, 64, (int)a.Kpad, (int)b.Kpad).total <= 160 * 1024 - kPairStaticLds;
 }
 
 template <int ACTA, int ACTB>
@@ -3417,7 +3517,7 @@ static void launch_pair_t(const float* x, const int8_t* WA, const int8_t* WB, co
   const void* fn = reinterpret_cast<const void*>(&conv_pool_pair_kernel<32, 64, ACTA, ACTB>);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 64) != hipSuccess)
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - kPairStaticLds) != hipSuccess)
       throw std::runtime_error("conv pair: the dynamic LDS limit could not be raised");
     attr_set = true;
   }
