@@ -2344,6 +2344,11 @@ __device__ __forceinline__ uint32_t wave_max_xlane(uint32_t v) {
   return t > v ? t : v;
 }
 
+// n / d for a divisor d the whole block shares, as a high multiply:
+// mag = ceil(2^32 / d) (div_magic), exact whenever n * d < 2^32.
+__device__ __forceinline__ uint32_t div_magic(uint32_t d) { return d <= 1 ? 0u : 0xffffffffu / d + 1u; }
+__device__ __forceinline__ int udiv(int n, uint32_t mag) { return mag ? (int)__umulhi((uint32_t)n, mag) : n; }
+
 __device__ __forceinline__ float tiny_epi(int32_t acc, float cs, float b, int act, float p) {
   switch (act) {
     case rgmath::ACT_RELU: return epi_value<rgmath::ACT_RELU>(acc, cs, b, p);
@@ -2376,9 +2381,14 @@ __global__ __launch_bounds__(tiny::kThreads) void mlp_tiny_kernel(const float* _
   // the other slot set (clear_slots without its block-size read, whose wait
   // would also wait for the copies above)
   for (int64_t i = tid; i < clear.n; i += tiny::kThreads) clear.p[i] = 0u;
+  // the i8 operand starts as zeros: each layer then writes only the words
+  // that hold its inputs or that an earlier layer left nonzero
+  for (int i = tid; i < kTinyRows * tiny::kQaLd / 16; i += tiny::kThreads) reinterpret_cast<v4i*>(qa)[i] = v4i{0, 0, 0, 0};
   wait_vmcnt<0>();
   __syncthreads();
   int cur = 0, ld = ch.l[0].in_f;  // the current activation buffer and its row stride
+  int qw = 0;                      // operand words per row that may be nonzero
+  const uint32_t rows_mag = div_magic((uint32_t)rows);
   for (int l = 0, woff = 0; l < ch.n; l++) {
     const TinyLayer L = ch.l[l];
     const float* src = act[cur];
@@ -2386,8 +2396,9 @@ __global__ __launch_bounds__(tiny::kThreads) void mlp_tiny_kernel(const float* _
     // per-wave partials were left in red by the previous layer's epilogue.
     if (l == 0) {
       uint32_t m0 = 0;
+      const uint32_t in_mag = div_magic((uint32_t)L.in_f);
       for (int e = tid; e < rows * L.in_f; e += tiny::kThreads) {
-        const int r = e / L.in_f, k = e - r * L.in_f;
+        const int r = udiv(e, in_mag), k = e - r * L.in_f;
         const uint32_t key = rgmath::absmax_key(src[r * ld + k]);
         m0 = key > m0 ? key : m0;
       }
@@ -2401,15 +2412,20 @@ __global__ __launch_bounds__(tiny::kThreads) void mlp_tiny_kernel(const float* _
     const float scale = rgmath::scale_from_absmax(rgmath::bitsf(m));
     const float inv = 1.0f / scale;
     if (tid == 0 && L.slot) L.slot[0] = m;
-    const int kp4 = L.kpad / 4;
-    for (int e = tid; e < rows * kp4; e += tiny::kThreads) {
-      const int r = e / kp4, w = e - r * kp4, k = 4 * w;
+    // words [0, kq) hold the inputs (zeros past in_f); words up to the
+    // previous layer's kq are rewritten as zeros; the rest are still zero
+    const int kq = (L.in_f + 3) / 4, wq = kq > qw ? kq : qw;
+    const uint32_t wq_mag = div_magic((uint32_t)wq);
+    for (int e = tid; e < rows * wq; e += tiny::kThreads) {
+      const int r = udiv(e, wq_mag), w = e - r * wq, k = 4 * w;
       float v[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) v[c] = k + c < L.in_f ? src[r * ld + k + c] : 0.0f;
       reinterpret_cast<uint32_t*>(qa + r * tiny::kQaLd)[w] = pack4(v[0], v[1], v[2], v[3], inv);
     }
+    qw = kq;
     __syncthreads();
+    const int ks = (L.in_f + 15) / 16;  // 16-byte steps that hold inputs; the rest of Kpad is zero
     const float cs = scale * L.w_scale;
     const bool last = l + 1 == ch.n;
     float* const dst = act[cur ^ 1];
@@ -2417,23 +2433,28 @@ __global__ __launch_bounds__(tiny::kThreads) void mlp_tiny_kernel(const float* _
     // take consecutive operand rows
     uint32_t mo = 0;  // absmax of the outputs this thread writes (the next layer's input)
     for (int e = tid; e < rows * L.out_f; e += tiny::kThreads) {
-      const int n = e / rows, r = e - n * rows;
+      const int n = udiv(e, rows_mag), r = e - n * rows;
       const v4i* qr = reinterpret_cast<const v4i*>(qa + r * tiny::kQaLd);
       const v4i* wr = reinterpret_cast<const v4i*>(wl + woff + n * kTinyWidth);
-      // Kpad == kTinyWidth: every fragment read is issued before the sums
+      // the steps that hold inputs (the zero ones add nothing to the exact
+      // sum); every fragment read is issued before the sums
       v4i a[kTinyWidth / 16], b[kTinyWidth / 16];
 #pragma unroll
       for (int k = 0; k < kTinyWidth / 16; k++) {
-        a[k] = qr[k];
-        b[k] = wr[k];
+        if (k < ks) {
+          a[k] = qr[k];
+          b[k] = wr[k];
+        }
       }
       int32_t acc = 0;
 #pragma unroll
       for (int k = 0; k < kTinyWidth / 16; k++) {
-        acc = __builtin_amdgcn_sdot4(a[k][0], b[k][0], acc, false);
-        acc = __builtin_amdgcn_sdot4(a[k][1], b[k][1], acc, false);
-        acc = __builtin_amdgcn_sdot4(a[k][2], b[k][2], acc, false);
-        acc = __builtin_amdgcn_sdot4(a[k][3], b[k][3], acc, false);
+        if (k < ks) {
+          acc = __builtin_amdgcn_sdot4(a[k][0], b[k][0], acc, false);
+          acc = __builtin_amdgcn_sdot4(a[k][1], b[k][1], acc, false);
+          acc = __builtin_amdgcn_sdot4(a[k][2], b[k][2], acc, false);
+          acc = __builtin_amdgcn_sdot4(a[k][3], b[k][3], acc, false);
+        }
       }
       const float v = tiny_epi(acc, cs, bias[l * kTinyWidth + n], L.act, L.act_param);
       if (last) {
@@ -2537,10 +2558,6 @@ static ConvBand conv_band_geom(const ConvShape& cs, int TM, int TN) {
   return ConvBand{(int)rows, bytes > (1 << 30) ? (1 << 30) : (int)bytes};
 }
 
-// n / d for a divisor d the whole block shares, as a high multiply:
-// mag = ceil(2^32 / d) (div_magic), exact whenever n * d < 2^32.
-__device__ __forceinline__ uint32_t div_magic(uint32_t d) { return d <= 1 ? 0u : 0xffffffffu / d + 1u; }
-__device__ __forceinline__ int udiv(int n, uint32_t mag) { return mag ? (int)__umulhi((uint32_t)n, mag) : n; }
 
 // The block's absmax for the next op: the 4 waves' maxima meet in LDS and
 // one atomic per block raises the image's slot (per image) or one partial of
