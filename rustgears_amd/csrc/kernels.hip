@@ -2039,24 +2039,26 @@ void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N
 // (K split over more workgroups, the slices added by another kernel), one
 // workgroup of 16 waves owns a 16 x TN output block (TN 16 or 64) and a
 // slice of K (usually all of it).
-//  * Its waves take the slice's K steps of 64 (wave, wave + 16, ...), R at
-//    a time.  Per step a lane loads 16 f32 inputs of row l % 16 as four
-//    16-byte loads at K 16 g + 4 (l / 16) (g = 0..3), so that each load
-//    instruction reads 64 contiguous bytes of each of the 16 rows, and
-//    quantizes them as quant_rows_kernel does (QuantTensor::from_f32 with
-//    the producer's absmax, quantize.rs:18-24; quantize_rz_bounded, since
-//    the scale comes from the absmax of these very values).  A 4 x 4
-//    transpose over the lane quads (v_permlane32_swap, v_permlane16_swap)
-//    then gives lane l the K bytes [16 (l / 16), +16) of its row, the
-//    v_mfma_i32_16x16x64_i8 operand layout, and the weight rows are loaded
-//    in that layout directly.  The first round's loads are issued before
-//    the scale is folded from its slot, so the two round trips overlap.
+//  * Its waves take the slice's K steps of 64, one per wave at a time.  A
+//    lane's operand is 16 f32 inputs of row l % 16, columns 16 g + 4 (l / 16)
+//    of the step (g = 0..3), quantized as quant_rows_kernel does
+//    (QuantTensor::from_f32 with the producer's absmax, quantize.rs:18-24;
+//    quantize_rz_bounded, since the scale comes from the absmax of these
+//    very values); a 4 x 4 transpose over the lane quads (v_permlane32_swap,
+//    v_permlane16_swap) then gives lane l the K bytes [16 (l / 16), +16) of
+//    its row, the v_mfma_i32_16x16x64_i8 operand layout, in which the
+//    weight rows are read directly.
+//  * Slices of 16 or more steps go through LDS in chunks of 16 steps copied
+//    by buffer loads with the LDS as destination, each instruction one
+//    contiguous KiB of a row; shorter slices load the fragments straight
+//    into registers.  The loads are issued before the scale is folded from
+//    its slot, so the two round trips overlap.
 //  * The waves' exact i32 sums are added in LDS (integer addition: any
 //    order gives the same sum), one output per thread.
 //  * With one slice the thread applies the fused epilogue of the large GEMM
 //    (quantize.rs:104-113), stores y and raises the next op's absmax.  With
 //    S slices (few blocks and a long K) each thread adds its sum to its
-//    output's 64-bit word in acc (zero at the start of the run) with one
+//    output's 64-bit word in acc64 (zero at the start of the run) with one
 //    device-scope atomic that returns the word's old value: the word's high
 //    bits count the slices added, its low 40 bits the sums plus 2^31 each
 //    (every term in [0, 2^32), so S <= 16 of them cannot carry into the
@@ -2072,6 +2074,11 @@ void launch_gemm_narrow_xq(const float* x, const int8_t* B, int64_t M, int64_t N
 namespace xqs {
 constexpr int kWaves = 16, kThreads = kWaves * 64, kTM = 16;
 constexpr int kMaxBlocks = 512, kTargetGrid = 256, kMaxSlices = 16;
+// LDS staging: a chunk of kChunk K steps (1 KiB of weights per row, 4 KiB of
+// f32 inputs per row), rows padded by 16 bytes so that the 16 rows of a
+// fragment read fall in different banks
+constexpr int kChunk = 16, kALd = kChunk * 64 * 4 + 16, kBLd = kChunk * 64 + 16;
+constexpr int kStageBytes = kTM * kALd + 64 * kBLd;
 }  // namespace xqs
 
 // Dword g of lane quad q (lanes 16 q .. 16 q + 15) <-> dword q of lane quad g.
@@ -2083,14 +2090,18 @@ __device__ __forceinline__ void quad_transpose(v4i& d) {
   d = v4i{(int32_t)c[0], (int32_t)c[1], (int32_t)e[0], (int32_t)e[1]};
 }
 
-template <int TN, int R>
+template <int TN>
 __global__ __launch_bounds__(xqs::kThreads) void gemm_xq_small_kernel(
     const float* __restrict__ x, const int8_t* __restrict__ B, int M, int N, int xk, int Kpad, int tiles_m,
     int tiles_n, int ks, Epilogue ep, uint64_t* __restrict__ acc64) {
   using namespace xqs;
   constexpr int NB = TN / 16, LD = TN + 4, OUT = kTM * TN;  // LD: the 4 lane quads' rows in different banks
   static_assert(OUT <= kThreads, "one output per thread");
-  __shared__ int32_t red[kWaves * kTM * LD];
+  static_assert(kWaves * kTM * LD * 4 <= kStageBytes, "the wave sums reuse the staging area");
+  __shared__ __attribute__((aligned(16))) int8_t smem[kStageBytes];
+  int8_t* const sa = smem;                  // [16 rows][kALd]: f32 inputs of a chunk
+  int8_t* const sb = smem + kTM * kALd;     // [TN rows][kBLd]: weight bytes of a chunk
+  int32_t* const red = reinterpret_cast<int32_t*>(smem);
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = (int)gridDim.x, tiles = tiles_m * tiles_n, S = G / tiles;
   int t = (int)blockIdx.x;
@@ -2105,56 +2116,104 @@ __global__ __launch_bounds__(xqs::kThreads) void gemm_xq_small_kernel(
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(B + (int64_t)n0 * Kpad), 0, TN * Kpad, 0x00020000);
   const int r = lane & 15, q = lane >> 4;
-  const uint32_t aoff = (uint32_t)(r * xk) * 4u + (uint32_t)q * 16u, boff = (uint32_t)(r * Kpad + q * 16);
   const int nk = Kpad / 64, kb = z * ks, ke = min(nk, kb + ks);
   v4i acc[NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) acc[j] = v4i{0, 0, 0, 0};
-  v4f af[R][4];
-  v4i bf[R][NB];
-  auto load_round = [&](int s0) {
+  // A lane's 16 inputs of a K step (row l % 16, columns 16 g + 4 (l / 16) of
+  // the step, g = 0..3), quantized (quant_rows_kernel's rule with the
+  // producer's scale) and transposed over the lane quads into the MFMA
+  // operand layout.
+  auto quantize_frag = [&](const v4f (&f)[4], float inv) {
+    v4i av;
 #pragma unroll
-    for (int u = 0; u < R; u++) {
-      const int s = s0 + u * kWaves, k0 = s * 64;
-      if (s >= ke) break;  // wave-uniform
+    for (int g = 0; g < 4; g++) {
+      const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(f[g][0] * inv);
+      const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(f[g][1] * inv);
+      const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(f[g][2] * inv);
+      const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(f[g][3] * inv);
+      const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u), hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+      av[g] = (int32_t)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+    quad_transpose(av);
+    return av;
+  };
+  float sa_scale;
+  if (ke - kb < kChunk) {
+    // A slice of fewer than kChunk steps (at most one per wave): each lane
+    // loads its fragments straight into registers -- four 16-byte loads of
+    // its inputs, one 16-byte load per weight row block -- all issued before
+    // the scale is folded.
+    const int s = kb + wave;
+    v4f f[4];
+    v4i bfr[NB];
+    if (s < ke) {
+      const uint32_t aoff = (uint32_t)(r * xk) * 4u + (uint32_t)q * 16u;
 #pragma unroll
       for (int g = 0; g < 4; g++)
-        af[u][g] = __builtin_bit_cast(
+        f[g] = __builtin_bit_cast(
             v4f, __builtin_amdgcn_raw_buffer_load_b128(
-                     ra, (int)(k0 + 16 * g + 4 * q < xk ? aoff + (uint32_t)(k0 + 16 * g) * 4u : kDropOffset), 0, 0));
+                     ra, (int)(s * 64 + 16 * g + 4 * q < xk ? aoff + (uint32_t)(s * 64 + 16 * g) * 4u : kDropOffset), 0,
+                     0));
 #pragma unroll
       for (int j = 0; j < NB; j++)
-        bf[u][j] = __builtin_bit_cast(
-            v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, (int)(boff + (uint32_t)(j * 16 * Kpad + k0)), 0, 0));
+        bfr[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rb, (int)((uint32_t)((j * 16 + r) * Kpad + s * 64 + 16 * q)), 0, 0));
     }
-  };
-  auto mma_round = [&](int s0, float inv) {
+    sa_scale = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
+    if (s < ke) {
+      const v4i av = quantize_frag(f, 1.0f / sa_scale);
 #pragma unroll
-    for (int u = 0; u < R; u++) {
-      if (s0 + u * kWaves >= ke) break;
-      v4i av;
+      for (int j = 0; j < NB; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bfr[j], acc[j], 0, 0, 0);
+    }
+  } else {
+    // Chunks of kChunk K steps through LDS.  The copies are buffer loads
+    // with the LDS as their destination, 1 KiB per instruction (64 lanes x
+    // 16 bytes): wave w copies input row w (up to four 1 KiB quarters of 256
+    // floats, the ones the slice reaches; floats past K get an offset past
+    // the buffer, so they land as zeros, as do rows past M) and weight rows
+    // w, w + 16, ... (1 KiB each).  Every instruction reads one contiguous
+    // KiB, where register loads of the fragments read 64 bytes of each of 16
+    // rows (C's fc layer: 9.1 -> 8.0 us).
+    float inv = 0.0f;
+    sa_scale = 0.0f;
+    for (int c0 = kb; c0 < ke; c0 += kChunk) {
+      const int kf0 = c0 * 64;  // first input column of the chunk
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const uint32_t b0 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][0] * inv);
-        const uint32_t b1 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][1] * inv);
-        const uint32_t b2 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][2] * inv);
-        const uint32_t b3 = (uint32_t)rgmath::quantize_rz_bounded(af[u][g][3] * inv);
-        const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u), hi = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
-        av[g] = (int32_t)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      for (int u = 0; u < 4; u++) {
+        if (kf0 + u * 256 >= ke * 64) break;  // past the slice
+        const int k = kf0 + u * 256 + lane * 4;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (RG_LDS_AS void*)(sa + wave * kALd + u * 1024), 16,
+            (int)(k < xk ? (uint32_t)(wave * xk + k) * 4u : kDropOffset), 0, 0, 0);
       }
-      quad_transpose(av);
 #pragma unroll
-      for (int j = 0; j < NB; j++) acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bf[u][j], acc[j], 0, 0, 0);
+      for (int u = 0; u < TN / kWaves; u++) {
+        const int row = wave + u * kWaves;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (RG_LDS_AS void*)(sb + row * kBLd), 16,
+                                                 (int)((uint32_t)(row * Kpad + kf0 + lane * 16)), 0, 0, 0);
+      }
+      if (c0 == kb) {  // the scale, folded while the first chunk is in flight
+        sa_scale = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
+        inv = 1.0f / sa_scale;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      const int s = c0 + wave;  // this wave's K step of the chunk
+      if (s < ke) {
+        const int ko = (s - c0) * 64;  // its first column within the chunk
+        v4f f[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) f[g] = *reinterpret_cast<const v4f*>(sa + r * kALd + (ko + 16 * g + 4 * q) * 4);
+        const v4i av = quantize_frag(f, inv);
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+          const v4i bf = *reinterpret_cast<const v4i*>(sb + (j * 16 + r) * kBLd + ko + 16 * q);
+          acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bf, acc[j], 0, 0, 0);
+        }
+      }
+      __syncthreads();  // the chunk's reads are done before the next copies (or the sums) overwrite it
     }
-  };
-  int s0 = kb + wave;
-  load_round(s0);
-  const float sa = rgmath::scale_from_absmax(rgmath::bitsf(wave_max_u32(part)));
-  const float inv = 1.0f / sa;
-  mma_round(s0, inv);
-  for (s0 += kWaves * R; s0 < ke; s0 += kWaves * R) {
-    load_round(s0);
-    mma_round(s0, inv);
   }
   // result register i of lane l: D[4 (l / 16) + i][l % 16] of block j
 #pragma unroll
@@ -2162,6 +2221,7 @@ __global__ __launch_bounds__(xqs::kThreads) void gemm_xq_small_kernel(
 #pragma unroll
     for (int i = 0; i < 4; i++) red[wave * (kTM * LD) + (4 * q + i) * LD + j * 16 + r] = acc[j][i];
   __syncthreads();
+  const float sa_s = sa_scale;
   const int orow = tid / TN, ocol = tid % TN;
   const bool mine = tid < OUT;
   int32_t sum = 0;
@@ -2182,7 +2242,7 @@ __global__ __launch_bounds__(xqs::kThreads) void gemm_xq_small_kernel(
   uint32_t amax = 0;
   const int row = m0 + orow, col = n0 + ocol;
   if (done && row < M && col < N) {
-    const float cs = sa * ep.w_scale, b = ep.bias[col];
+    const float cs = sa_s * ep.w_scale, b = ep.bias[col];
     float v;
     switch (ep.act) {
       case rgmath::ACT_RELU: v = epi_value<rgmath::ACT_RELU>(sum, cs, b, ep.act_param); break;
@@ -2264,10 +2324,10 @@ void launch_gemm_xq_small(const float* x, const int8_t* B, int64_t M, int64_t N,
   uint64_t* const acc64 = reinterpret_cast<uint64_t*>(sync);
   const dim3 grid((unsigned)(g.S * g.tiles_m * g.tiles_n));
   if (g.TN == 16)
-    RG_LAUNCH((gemm_xq_small_kernel<16, 4>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
+    RG_LAUNCH((gemm_xq_small_kernel<16>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
               (int)Kpad, g.tiles_m, g.tiles_n, g.ks, ep, acc64);
   else
-    RG_LAUNCH((gemm_xq_small_kernel<64, 2>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
+    RG_LAUNCH((gemm_xq_small_kernel<64>), grid, dim3(xqs::kThreads), 0, s, x, B, (int)M, (int)N, (int)K,
               (int)Kpad, g.tiles_m, g.tiles_n, g.ks, ep, acc64);
 }
 
