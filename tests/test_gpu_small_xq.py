@@ -5,13 +5,15 @@ A Linear whose GEMM would otherwise have fewer than 128 tiles of 128 x 128
 and whose input's absmax its producer emitted (npu.rs:312 ->
 quantize.rs:18-24 with that absmax) runs as one kernel: one workgroup per
 16 x 16 (or 16 x 64) output block and K slice, quantizing the f32 input as
-it loads it, adding its waves' exact i32 sums in LDS, the last workgroup of
-a block adding the other slices' sums, and applying the fused epilogue
-(quantize.rs:104-113).  Each case's output must equal bit for bit the
+it loads it, adding its waves' exact i32 sums in LDS, the K slices meeting
+in one 64-bit counting atomic per output (the thread that completes the
+count applies the fused epilogue, quantize.rs:104-113).  Each case's output must equal bit for bit the
 oracle's and the output with the kernel turned off (RGNPU_SMALL_XQ=0:
 quant_rows, the tile GEMM and, when it splits K, its epilogue): the CNN's fc
-layer, one, four and eight K slices, both block widths, ragged rows (the last
-16-row block partly filled), K not a multiple of 64, N not a multiple of 16,
+layer, one, four and eight K slices, both block widths, slices staged in
+LDS in one and in two chunks (the second partial, K ending inside it) and
+slices short enough for register loads, ragged rows (the last 16-row block
+partly filled), K not a multiple of 64, N not a multiple of 16,
 every activation, and inputs that drive the scale to infinity or the
 activations to NaN.  Programs it does not take (K % 4 != 0, 128 tiles or
 more) run the tile GEMM.  The op's record has no launch before its GEMM when
@@ -93,6 +95,7 @@ CASES = [
     (17, (1024, 4096, 2048, 16), ("leaky", "sigmoid", "relu"), [1]),  # 64 x 4
     (16, (1024, 4096, 256), ("relu", "relu"), [1]),                 # 16 x 8
     (1000, (1024, 256, 160), ("relu", "leaky"), [1]),               # 64 x 1 (252 blocks)
+    (256, (1024, 7932, 256), ("relu", None), [1]),                   # 64 x 4: two LDS chunks, K 7932
 ]
 
 
