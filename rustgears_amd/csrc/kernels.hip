@@ -2014,6 +2014,9 @@ static void launch_gemm_narrow_t(const int8_t* A, const int8_t* B, int64_t M, in
   else if (N <= 8)
     RG_LAUNCH((gemm_narrow_kernel<8, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep,
               xk, q_out, scale_out);
+  else if (N <= 12)  // the 10-class heads: 12 weight rows per lane instead of 16
+    RG_LAUNCH((gemm_narrow_kernel<12, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes,
+              ep, xk, q_out, scale_out);
   else
     RG_LAUNCH((gemm_narrow_kernel<16, MODE, XQ>), dim3((unsigned)blocks), dim3(256), 0, s, A, B, M, N, Kpad_bytes, ep,
               xk, q_out, scale_out);
