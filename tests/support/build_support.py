@@ -1,14 +1,15 @@
 """Builds the standalone GPU programs of the test suite into
 tests/support/_build/ (hipcc, gfx950, same FP flags as the library):
-devmath_gpu_check (tests/test_gpu_devmath.py) and kloop_lab
-(tests/test_gpu_kloop_lab.py)."""
+devmath_gpu_check (tests/test_gpu_devmath.py), kloop_lab
+(tests/test_gpu_kloop_lab.py) and input_quant_lab
+(tests/test_gpu_input_quant_lab.py)."""
 import os
 import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "_build")
 EXE = os.path.join(OUT, "devmath_gpu_check")
-PROGRAMS = ["devmath_gpu_check", "kloop_lab"]
+PROGRAMS = ["devmath_gpu_check", "kloop_lab", "input_quant_lab"]
 
 
 def build() -> str:
