@@ -48,6 +48,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <stdexcept>
 
 #include "devmath.h"
@@ -1039,8 +1040,11 @@ bool input_quant_supported(int64_t M, int64_t K, int64_t Mpad, int64_t Kpad) {
 }
 
 // The launch: the smallest U (units kept per thread) whose grid of
-// ceil(W / (512 U)) workgroups is resident; else U = 64 on every resident
-// slot (capped by the barrier's kMaxGrid), the rest read twice.
+// ceil(W / (512 U)) workgroups is resident with at most one workgroup per CU
+// (fewer workgroups meet at the barrier: the deep MLP's 4096 x 896 operand
+// runs 224 workgroups of U = 8 instead of 448 of U = 4, 0.0470 -> 0.0457 ms
+// per step); else the smallest U whose grid is resident; else U = 64 on every
+// resident slot (capped by the barrier's kMaxGrid), the rest read twice.
 struct IqLaunch {
   int U;
   int64_t G;
@@ -1057,13 +1061,32 @@ static int64_t iq_cap() {
   return cap < rqk::kMaxGrid ? cap : rqk::kMaxGrid;
 }
 
+static int64_t iq_cus() {
+  static const int64_t cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    return (int64_t)n;
+  }();
+  return cus;
+}
+
 static IqLaunch input_quant_choice(int64_t Mpad, int64_t Kpad) {
   const int64_t W = Mpad * Kpad / 4;
   const int64_t caps[5] = {iq_cap<4>(), iq_cap<8>(), iq_cap<16>(), iq_cap<32>(), iq_cap<64>()};
-  for (int i = 0, U = 4; i < 5; i++, U *= 2) {
-    const int64_t per_block = (int64_t)iq::kThreads * U, G = (W + per_block - 1) / per_block;
-    if (G <= caps[i]) return IqLaunch{U, G < 1 ? 1 : G};
-  }
+  // RGNPU_IQ_U (4 .. 64, measurement): no U below it
+  static const int min_u = [] {
+    const char* e = getenv("RGNPU_IQ_U");
+    return e ? atoi(e) : 0;
+  }();
+  for (int pass = 0; pass < 2; pass++)
+    for (int i = 0, U = 4; i < 5; i++, U *= 2) {
+      if (U < min_u) continue;
+      const int64_t per_block = (int64_t)iq::kThreads * U, G = (W + per_block - 1) / per_block;
+      const int64_t limit = pass == 0 && iq_cus() < caps[i] ? iq_cus() : caps[i];
+      if (G <= limit) return IqLaunch{U, G < 1 ? 1 : G};
+    }
   return IqLaunch{64, caps[4]};
 }
 
