@@ -113,3 +113,32 @@ def test_staged_input_small_output_and_concurrency(rg):
     for i, (g, w) in enumerate(zip(got, want * 3)):
         assert_bitexact_f32(g, w, f"concurrent staged run {i}")
     sess.close()
+
+
+@pytest.mark.parametrize("name", ["cnn", "quickstart"])
+def test_concurrent_runs_of_one_kernel_programs(rg, ref, name):
+    """Six threads on the CNN (both convs and pools in one workgroup per
+    image, the fc layer adding its K slices through counting atomics in the
+    run's slot set, the head quantizing its input as it reads it) and on the
+    quickstart MLP (the whole program in one workgroup): two batch sizes and
+    input magnitudes interleaved, every result bit-exact with the serial run
+    of the same input and the serial runs with the oracle."""
+    from rustgears_amd import configs
+    if name == "cnn":
+        model, x0 = configs.cnn(n=256)
+        sizes = [256, 96]
+    else:
+        model, x0 = configs.quickstart(rows=64)
+        sizes = [64, 17]
+    layers = model.export()
+    sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
+    inputs = [(rg.randn([sizes[i % 2]] + list(x0.shape[1:])) * (0.1 + i)).astype(np.float32) for i in range(6)]
+    want = [sess.run(x) for x in inputs]
+    print(f"[concurrency] {name}: 6 threads x {3 * len(inputs)} runs", flush=True)
+    with ThreadPoolExecutor(6) as ex:
+        got = list(ex.map(sess.run, inputs * 3))
+    for i, (g, w) in enumerate(zip(got, want * 3)):
+        assert_bitexact_f32(g, w, f"{name} run {i}")
+    for i in range(2):
+        assert_bitexact_f32(want[i], ref.RefProgram(layers).run(inputs[i], parallel=True), f"{name} {i} vs oracle")
+    sess.close()
