@@ -471,9 +471,17 @@ def _random_model(seed):
 def test_random_models(rg, ref, seed):
     """Seeded random layer stacks through the whole plan (buffer ping-pong,
     slot layout, fusion and folding rules, every kernel choice): every op
-    bit-exact with the oracle."""
+    bit-exact with the oracle in capture mode, then the output of the
+    production plan (no capture: the whole-program MLP, the small-tile GEMM
+    quantizing as it loads, the fused requantization, the quantizing GEMVs and
+    narrow heads, where the shapes take them) bit-exact with the same."""
     layers, x = _random_model(1000 + seed)
-    check_against_oracle(rg, ref, layers, x, f"random model {seed}: {[type(l).__name__ for l in layers]}")
+    what = f"random model {seed}: {[type(l).__name__ for l in layers]}"
+    y = check_against_oracle(rg, ref, layers, x, what)
+    print(f"[parity] {what} production plan", flush=True)
+    sess = make_session(rg, layers)
+    assert_bitexact_f32(sess.run(x), y, what + " production plan")
+    sess.close()
 
 
 def test_reference_integration_model(rg, ref):
