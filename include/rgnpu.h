@@ -223,7 +223,8 @@ int64_t rgnpu_program_op_weight(const rgnpu_program* prog, int64_t i, int8_t* ds
  *    in memory: the i8 activations of a Linear whose operand buffer was
  *    written (not for the GEMMs that quantize as they read, nor for convs,
  *    which quantize into LDS), the scale(s) from the absmax the consumer
- *    read, and the f32 output of ops that store theirs (not of a GEMM that
+ *    read (none for a one-row GEMV that measures its own input's absmax in
+ *    registers), and the f32 output of ops that store theirs (not of a GEMM that
  *    writes the next op's operand instead, nor of a conv that pools in its
  *    epilogue: the MaxPool2d op then shows the pooled output).  The i32
  *    accumulators are never available; what is not available reads as 0

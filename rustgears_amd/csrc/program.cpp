@@ -205,7 +205,7 @@ struct Plan {
   // whether its i8 operand (cap_q) and f32 output (cap_out) exist in memory
   // on the production path.
   std::vector<std::unique_ptr<DevBuf>> tap_slot;
-  std::vector<uint8_t> tap_q_ok, tap_out_ok;
+  std::vector<uint8_t> tap_q_ok, tap_out_ok, tap_scale_ok;
   bool taps_ready = false;
   // Per op, indices into the run's launch events (-1 = the run-start event):
   // [0] last launch before the op, [1] last launch before its main kernel,
@@ -1114,6 +1114,7 @@ static void ensure_tap_buffers(rgnpu_program* P, Plan& plan) {
   plan.tap_slot.resize(n);
   plan.tap_q_ok.assign(n, 0);
   plan.tap_out_ok.assign(n, 0);
+  plan.tap_scale_ok.assign(n, 1);
   for (size_t i = 0; i < n; i++) {
     const Op& op = *P->ops[i];
     const OpPlan& pl = plan.ops[i];
@@ -1373,6 +1374,9 @@ static void enqueue(rgnpu_program* P, Plan& plan, const float* x, float* y, hipE
         // absmax or, when its input has none yet, the input's own.
         const bool gemv_xq = pl.gemv && !pl.q_ready && gemv_xq_supported(pl.rows, op.in_f, op.Kpad, in);
         const bool small_xq = pl.small_xq && !cap && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+        // a one-row GEMV that measures its input's absmax itself keeps it in
+        // registers: no slot holds it
+        if (tap) plan.tap_scale_ok[i] = !(gemv_xq && pl.explicit_absmax);
         if (narrow_xq || gemv_xq || small_xq) {
           // nothing before the GEMM
         } else if (pl.iq_sync_base >= 0) {
@@ -2113,7 +2117,7 @@ int64_t rgnpu_program_capture(rgnpu_program* P, int64_t i, int32_t what, void* d
         case RGNPU_CAP_ACC:
           return 0;  // the i32 sums never leave the GEMM's registers
         case RGNPU_CAP_SCALE: {
-          if (!gemm) return 0;
+          if (!gemm || !plan.tap_scale_ok[(size_t)i]) return 0;
           // the scale each consumer derives from the absmax slot that its
           // producer (or its own absmax pass) filled
           const bool lin = op.kind == OP_LINEAR;

@@ -11,14 +11,16 @@ exists in memory after each op:
   previous GEMM's fused requantization, with the certified GELU form for
   GELU producers;
 * the scale every quantizing op derived from its absmax slot (per tensor for
-  a Linear, per image for a conv, npu.rs:346-351);
+  a Linear, per image for a conv, npu.rs:346-351); a one-row GEMV that
+  measures its own input's absmax keeps it in registers, so it has none;
 * the f32 output of every op that stores one (a conv + pool kernel stores
   only the pooled output, the MaxPool2d op's; the CNN's two conv + pool
   stages run as one kernel that keeps the first pool's output in LDS).
 
 Each is compared bit for bit with the oracle's capture of the same op, at
 the benchmark's full sizes: the 4 x 4096^2 GELU stack (8192 rows), the deep
-MLP (4096 rows) and the CNN (256 images).
+MLP (4096 rows), the CNN (256 images) and the decode-shape GEMVs (one and
+eight rows).
 """
 import numpy as np
 import pytest
@@ -28,10 +30,11 @@ from conftest import assert_bitexact_f32
 pytestmark = pytest.mark.gpu
 
 
-def _check_production(rg, ref, layers, x, what, want_q, want_out):
+def _check_production(rg, ref, layers, x, what, want_q, want_out, no_scale=()):
     """Runs the production path with taps and the oracle with capture; checks
     every available tap and that exactly the expected ones exist (want_q /
-    want_out: op indices with an i8 operand / an f32 output in memory)."""
+    want_out: op indices with an i8 operand / an f32 output in memory;
+    no_scale: quantizing ops whose absmax no slot holds)."""
     print(f"[taps] {what} x{tuple(x.shape)}", flush=True)
     sess = rg.InferenceSession.from_layers(layers, rg.ExecutionProvider.mi355x_int8())
     y_plain = sess.run(x)
@@ -55,7 +58,9 @@ def _check_production(rg, ref, layers, x, what, want_q, want_out):
             checked += q.size
         s = sess.capture(i, 1)
         ws = prog.capture(i, 1)
-        if ws.size:
+        if i in no_scale:
+            assert ws.size and s.size == 0, tag + ": the scale is not in memory"
+        elif ws.size:
             assert_bitexact_f32(s, ws, tag + " scale")
         o = sess.capture(i, 3)
         if o.size:
@@ -109,3 +114,16 @@ def test_cnn_production_operands(rg, ref):
                                                  "NPU::MaxPool2d", "NPU::Flatten", "NPU::FusedGemmAct",
                                                  "NPU::Gemm"], labels
     _check_production(rg, ref, layers, x, "cnn", [], [3, 4, 5, 6])
+
+
+@pytest.mark.parametrize("batch,want_q,no_scale", [(1, [1], [0]), (8, [0, 1], [])], ids=["b1", "b8"])
+def test_gemv_production_operands(rg, ref, batch, want_q, no_scale):
+    """G (8192 -> 28672 SiLU -> 8192): at one row, layer 1 measures and
+    quantizes its own input as it stages it (neither its operand nor its
+    absmax is in memory) and quant_rows writes layer 2's operand from layer
+    1's output; at eight rows the one-pass input quantization writes layer
+    1's operand and quant_rows layer 2's, both read by the matrix-core GEMV.
+    Both layers' f32 outputs are in memory."""
+    from rustgears_amd import configs
+    layers, x = configs.gemv(batch=batch)
+    _check_production(rg, ref, layers, x, f"gemv b{batch}", want_q, [0, 1], no_scale)
