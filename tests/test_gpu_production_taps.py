@@ -19,8 +19,8 @@ exists in memory after each op:
 
 Each is compared bit for bit with the oracle's capture of the same op, at
 the benchmark's full sizes: the 4 x 4096^2 GELU stack (8192 rows), the deep
-MLP (4096 rows), the CNN (256 images) and the decode-shape GEMVs (one and
-eight rows).
+MLP (4096 rows), the CNN (256 images), the decode-shape GEMVs (one and
+eight rows) and the quickstart MLP (64 rows).
 """
 import numpy as np
 import pytest
@@ -127,3 +127,13 @@ def test_gemv_production_operands(rg, ref, batch, want_q, no_scale):
     from rustgears_amd import configs
     layers, x = configs.gemv(batch=batch)
     _check_production(rg, ref, layers, x, f"gemv b{batch}", want_q, [0, 1], no_scale)
+
+
+def test_quickstart_production_operands(rg, ref):
+    """Q (64 rows, 4 -> 32 + BN + ReLU -> 3) runs as one workgroup: both
+    operands and the hidden activations stay in LDS, only the program's
+    output is in memory; each layer's absmax is written to its slot, so both
+    scales are tapped."""
+    from rustgears_amd import configs
+    model, x = configs.quickstart()
+    _check_production(rg, ref, model.export(), x, "quickstart", [], [1])
