@@ -978,8 +978,11 @@ static std::unique_ptr<Plan> make_plan(rgnpu_program* P, const int64_t* shape, i
     any_requant = true;  // the second operand buffer
   }
   // A Linear that quantizes its own input does so in one pass when the
-  // shapes fit the kernel's 32-bit offsets.
-  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8 && persistent_ok; i++) {
+  // shapes fit the kernel's 32-bit offsets (RGNPU_INPUT_QUANT=0, for
+  // measurement: the absmax and quantize kernels instead).
+  const char* iqe = getenv("RGNPU_INPUT_QUANT");
+  const bool one_pass = !(iqe && atoi(iqe) == 0);
+  for (size_t i = 0; i < nops && P->precision == RGNPU_PRECISION_INT8 && persistent_ok && one_pass; i++) {
     const Op& op = *P->ops[i];
     OpPlan& pl = plan->ops[i];
     if (op.kind != OP_LINEAR || !pl.explicit_absmax || pl.rows <= 0 ||
