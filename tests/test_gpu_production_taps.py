@@ -137,3 +137,19 @@ def test_quickstart_production_operands(rg, ref):
     from rustgears_amd import configs
     model, x = configs.quickstart()
     _check_production(rg, ref, model.export(), x, "quickstart", [], [1])
+
+
+@pytest.mark.parametrize("rows,k", [(1024, 1024), (2048, 1536), (3072, 2048), (4096, 3072), (6144, 4096)],
+                         ids=["U4", "U8", "U16", "U32", "U64"])
+def test_input_quantization_every_grid_shape(rg, ref, rows, k):
+    """The one-pass input quantization keeps U = 4, 8, 16, 32 or 64 units
+    per thread, the smallest whose grid fits one workgroup per CU (192
+    workgroups here, 128 for U = 4): a Linear(k, 40) + ReLU on rows x k
+    inputs that select each U, its i8 operand, scale and output bit-exact
+    with the oracle's."""
+    from rustgears_amd import nn
+    rg.manual_seed(rows + k)
+    layers = nn.Sequential().add(nn.Linear(k, 40)).add(nn.Relu()).export()
+    x = rg.randn([rows, k])
+    x[rows // 3, k - 1] = -41.5  # the absmax in the last unit of one row
+    _check_production(rg, ref, layers, x, f"input quant {rows}x{k}", [0], [0])
