@@ -907,6 +907,15 @@ __device__ __forceinline__ void iq_quantize_from(__amdgpu_buffer_rsrc_t rx, __am
 // b U 512 + t, 512 apart, then the remaining ones from G U 512 + b 512 + t,
 // G 512 apart.
 __device__ __forceinline__ uint32_t iq_kept0(uint32_t b, uint32_t t, int U) { return b * (uint32_t)U * 512u + t; }
+// The unit range of workgroup b: hardware deals workgroups round-robin over
+// the 8 XCDs (b on XCD b & 7), so with G a multiple of 8 the workgroups of
+// XCD x take the x-th contiguous eighth of the input (and write that eighth
+// of the operand, about half of the rows the consuming GEMM's XCD-grouped
+// tile order sends to XCD x).  On S (256 workgroups) the quantization went
+// from 34.2-34.4 to 31.7-31.8 us against ranges dealt round-robin.
+__device__ __forceinline__ uint32_t iq_range(uint32_t b, uint32_t G) {
+  return (G & 7u) == 0 ? (b & 7u) * (G >> 3) + (b >> 3) : b;
+}
 __device__ __forceinline__ uint32_t iq_rest0(uint32_t b, uint32_t t, int U, uint32_t G) {
   return G * (uint32_t)U * 512u + b * 512u + t;
 }
@@ -930,7 +939,8 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
   static_assert(kThreads == 512, "unit layout");
-  const uint32_t w0 = iq_kept0((uint32_t)b, (uint32_t)tid, U);
+  const uint32_t rb = iq_range((uint32_t)b, (uint32_t)G);
+  const uint32_t w0 = iq_kept0(rb, (uint32_t)tid, U);
   const __amdgpu_buffer_rsrc_t rx = bounded_rsrc(x);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(q, 0, (int)(sh.W * 4u), 0x00020000);
   const uint32_t r0 = w0 / sh.upr, c0 = w0 - r0 * sh.upr;
@@ -971,7 +981,7 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   for (int j = 0; j < KR; j++) m = iq_absmax(m, keep[j]);
   // the remaining units (an input larger than the grid keeps)
   const uint32_t NT = (uint32_t)G * kThreads;
-  const uint32_t rest_w = iq_rest0((uint32_t)b, (uint32_t)tid, U, (uint32_t)G);
+  const uint32_t rest_w = iq_rest0(rb, (uint32_t)tid, U, (uint32_t)G);
   const uint32_t rest_r = rest_w / sh.upr, rest_c = rest_w - rest_r * sh.upr;
   r = rest_r;
   c = rest_c;
@@ -1027,9 +1037,10 @@ __global__ __launch_bounds__(iq::kThreads) void input_quant_kernel(const float* 
   const uint32_t tid2 = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 64u +
                         __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   for (int d = 0; d < ndef; d++) {
-    const uint32_t k0 = iq_kept0(list[d], tid2, U), kr0 = k0 / sh.upr;
+    const uint32_t rd = iq_range(list[d], (uint32_t)G);
+    const uint32_t k0 = iq_kept0(rd, tid2, U), kr0 = k0 / sh.upr;
     iq_quantize_from<VEC>(rx, rq, sh, k0, (uint32_t)U, kr0, k0 - kr0 * sh.upr, sh.kr, sh.kc, inv);
-    const uint32_t q0 = iq_rest0(list[d], tid2, U, (uint32_t)G), qr0 = q0 / sh.upr;
+    const uint32_t q0 = iq_rest0(rd, tid2, U, (uint32_t)G), qr0 = q0 / sh.upr;
     iq_quantize_from<VEC>(rx, rq, sh, q0, ~0u, qr0, q0 - qr0 * sh.upr, sh.nr, sh.nc, inv);
   }
 }
